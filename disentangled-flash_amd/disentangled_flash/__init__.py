@@ -1,0 +1,24 @@
+"""DisentangledFlash for MI355X: fused DeBERTa-v2/v3 disentangled attention in HIP.
+
+Drop-in for the reference package's public API (``__init__.py:3-19``):
+``optimize_deberta``, ``enable_deberta_inference``, ``compile_deberta_buckets``,
+``DebertaV2InferenceEncoder`` and the ``DisentangledFlashAttention`` module.
+"""
+
+from .deberta import (
+    DebertaV2InferenceEncoder,
+    compile_deberta_buckets,
+    enable_deberta_inference,
+    optimize_deberta,
+)
+from .kernel import DisentangledFlashAttention
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "DebertaV2InferenceEncoder",
+    "DisentangledFlashAttention",
+    "compile_deberta_buckets",
+    "enable_deberta_inference",
+    "optimize_deberta",
+]

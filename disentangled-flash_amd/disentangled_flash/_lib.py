@@ -1,0 +1,113 @@
+"""ctypes binding of ``libdflash.so`` (the C ABI declared in ``include/dflash.h``).
+
+The library is a plain HIP shared object built for gfx950 next to this file.
+It is loaded after ``torch`` so that it binds to the HIP runtime torch already
+loaded (both resolve ``libamdhip64.so.7``), which keeps torch's streams and
+device pointers valid inside the library.
+
+There is no fallback: if the library is missing or cannot be loaded, every
+HIP-backend call raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime first)
+
+LIBRARY_NAME = "libdflash.so"
+ABI_VERSION = 1
+
+DTYPE_CODES = {
+    torch.float16: 0,
+    torch.bfloat16: 1,
+    torch.float32: 2,
+}
+
+_c_void_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_int64 = ctypes.c_int64
+_c_float = ctypes.c_float
+
+_handle: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+
+def library_path() -> Path:
+    override = os.environ.get("DFLASH_LIBRARY")
+    return Path(override) if override else Path(__file__).with_name(LIBRARY_NAME)
+
+
+def _bind(lib: ctypes.CDLL) -> None:
+    lib.dflash_attention_fwd.restype = _c_int
+    lib.dflash_attention_fwd.argtypes = [
+        _c_void_p, _c_void_p, _c_void_p,            # query, key, value
+        _c_void_p, _c_void_p,                        # c2p, p2c
+        _c_void_p, _c_void_p, _c_void_p,             # delta_to_local, mask, out
+        _c_int, _c_int, _c_int, _c_int, _c_int,      # B, H, L, D, S
+        _c_float, _c_int, _c_int, _c_int, _c_int,    # scale, has_c2p, has_p2c, dtype, strict
+        _c_void_p,                                   # stream
+    ]
+    lib.dflash_attention_rel_fwd.restype = _c_int
+    lib.dflash_attention_rel_fwd.argtypes = [
+        _c_void_p, _c_void_p, _c_void_p,             # query, key, value
+        _c_int64, _c_int64, _c_int64,                # stride_b, stride_h, stride_l
+        _c_void_p, _c_void_p,                        # pos_key, pos_query
+        _c_void_p, _c_void_p, _c_void_p,             # delta_to_local, mask, out
+        _c_int, _c_int, _c_int, _c_int, _c_int,      # B, H, L, D, S
+        _c_float, _c_int, _c_int, _c_int, _c_int,    # scale, has_c2p, has_p2c, dtype, strict
+        _c_void_p,                                   # stream
+    ]
+    lib.dflash_error_string.restype = ctypes.c_char_p
+    lib.dflash_error_string.argtypes = [_c_int]
+    lib.dflash_abi_version.restype = _c_int
+    lib.dflash_abi_version.argtypes = []
+
+
+def load() -> ctypes.CDLL:
+    """Load and bind the library once; raise ``RuntimeError`` if it is unusable."""
+
+    global _handle, _load_error
+    if _handle is not None:
+        return _handle
+    path = library_path()
+    if not path.exists():
+        _load_error = (
+            f"{path} is missing: build the HIP library first "
+            "(python __graft_entry__.py, or python disentangled-flash_amd/csrc/build.py)"
+        )
+        raise RuntimeError(_load_error)
+    try:
+        lib = ctypes.CDLL(str(path))
+        _bind(lib)
+    except (OSError, AttributeError) as error:
+        _load_error = f"cannot load {path}: {error}"
+        raise RuntimeError(_load_error) from error
+    version = lib.dflash_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    _handle = lib
+    return lib
+
+
+def is_available() -> bool:
+    try:
+        load()
+    except RuntimeError:
+        return False
+    return True
+
+
+def check(code: int, what: str) -> None:
+    if code != 0:
+        message = load().dflash_error_string(code).decode()
+        raise RuntimeError(f"{what} failed with code {code}: {message}")
+
+
+def current_stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+__all__ = ["DTYPE_CODES", "check", "current_stream_handle", "is_available", "library_path", "load"]

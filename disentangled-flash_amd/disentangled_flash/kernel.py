@@ -1,0 +1,405 @@
+"""HIP (gfx950) fused DeBERTa attention: op boundary and attention module.
+
+Two custom ops wrap the C ABI of ``libdflash.so``:
+
+* ``disentangled_flash::deberta_attention`` - same arguments and semantics as the
+  reference's ``gliner2_attention::deberta_attention`` (``kernel.py:368-438``):
+  head-major Q/K/V plus precomputed ``[B, H, L, S]`` c2p/p2c tables.
+* ``disentangled_flash::deberta_attention_rel`` - the MI355X design: the kernel
+  reads Q/K/V straight out of the fused QKV projection output ``[B, L, 3*H*d]``
+  and computes the relative scores from the ``[H, S, d]`` projected position
+  rows inside each tile, so neither the head reshape copies nor the two
+  ``[B, H, L, S]`` tables exist.
+
+Both ops register a fake (meta) implementation, so ``torch.compile(fullgraph=True)``
+traces through them the way the reference relies on ``triton_op``.
+
+``HipInferenceDisentangledSelfAttention`` mirrors ``TritonInferenceDisentangledSelfAttention``
+(``kernel.py:471-638``): same plan type, validation and error messages.
+"""
+
+from __future__ import annotations
+
+from typing import Any, NamedTuple
+
+import torch
+from torch.nn import functional as F
+
+from . import _lib
+from ._torch import TorchInferenceDisentangledSelfAttention
+from .modeling import DebertaAttentionConfig
+from .position import SharedPositionPlanCache, canonical_device
+
+LOG2E = 1.4426950408889634
+SUPPORTED_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+RELATIVE_MODES = ("fused", "table")
+
+
+@torch.library.custom_op("disentangled_flash::deberta_attention", mutates_args=())
+def deberta_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    c2p: torch.Tensor,
+    p2c: torch.Tensor,
+    delta_to_local: torch.Tensor,
+    attention_mask: torch.Tensor,
+    num_heads: int,
+    sequence_length: int,
+    active_slots: int,
+    score_scale_log2: float,
+    has_c2p: bool,
+    has_p2c: bool,
+    is_bf16: bool,
+    is_fp32: bool,
+    strict_fp32: bool,
+) -> torch.Tensor:
+    """Fused attention over precomputed c2p/p2c tables (reference op contract).
+
+    ``query/key/value`` are ``[B, H, L, d]`` contiguous, ``c2p/p2c`` are
+    ``[B, H, L, S]`` contiguous (ignored when their mode is off) and the
+    output is ``[B, L, H*d]`` in the input dtype.
+    """
+
+    lib = _lib.load()
+    batch, _, length, head_dim = query.shape
+    out = torch.empty(
+        (batch, sequence_length, num_heads * head_dim), device=query.device, dtype=query.dtype
+    )
+    code = lib.dflash_attention_fwd(
+        query.data_ptr(),
+        key.data_ptr(),
+        value.data_ptr(),
+        c2p.data_ptr() if has_c2p else None,
+        p2c.data_ptr() if has_p2c else None,
+        delta_to_local.data_ptr(),
+        attention_mask.data_ptr(),
+        out.data_ptr(),
+        batch,
+        num_heads,
+        sequence_length,
+        head_dim,
+        active_slots,
+        score_scale_log2,
+        int(has_c2p),
+        int(has_p2c),
+        _lib.DTYPE_CODES[query.dtype],
+        int(strict_fp32),
+        _lib.current_stream_handle(query.device),
+    )
+    _lib.check(code, "dflash_attention_fwd")
+    return out
+
+
+@deberta_attention.register_fake
+def _deberta_attention_fake(query, key, value, c2p, p2c, delta_to_local, attention_mask,
+                            num_heads, sequence_length, active_slots, score_scale_log2,
+                            has_c2p, has_p2c, is_bf16, is_fp32, strict_fp32):
+    batch, _, _, head_dim = query.shape
+    return query.new_empty((batch, sequence_length, num_heads * head_dim))
+
+
+@torch.library.custom_op("disentangled_flash::deberta_attention_rel", mutates_args=())
+def deberta_attention_rel(
+    qkv: torch.Tensor,
+    pos_key: torch.Tensor,
+    pos_query: torch.Tensor,
+    delta_to_local: torch.Tensor,
+    attention_mask: torch.Tensor,
+    num_heads: int,
+    head_dim: int,
+    score_scale_log2: float,
+    has_c2p: bool,
+    has_p2c: bool,
+    strict_fp32: bool,
+) -> torch.Tensor:
+    """Fused attention with in-kernel relative scores.
+
+    ``qkv`` is the fused projection output ``[B, L, 3*H*d]`` (Q, K, V column
+    blocks); ``pos_key/pos_query`` are ``[H, S, d]``.  When a mode is off its
+    position tensor is never read.  Output ``[B, L, H*d]``.
+    """
+
+    lib = _lib.load()
+    batch, length, width = qkv.shape
+    hd = num_heads * head_dim
+    out = torch.empty((batch, length, hd), device=qkv.device, dtype=qkv.dtype)
+    stride_b, stride_l = qkv.stride(0), qkv.stride(1)
+    base = qkv.data_ptr()
+    esize = qkv.element_size()
+    active = pos_key.size(1) if has_c2p else (pos_query.size(1) if has_p2c else 0)
+    code = lib.dflash_attention_rel_fwd(
+        base,
+        base + hd * esize,
+        base + 2 * hd * esize,
+        stride_b,
+        head_dim,
+        stride_l,
+        pos_key.data_ptr() if has_c2p else None,
+        pos_query.data_ptr() if has_p2c else None,
+        delta_to_local.data_ptr(),
+        attention_mask.data_ptr(),
+        out.data_ptr(),
+        batch,
+        num_heads,
+        length,
+        head_dim,
+        active,
+        score_scale_log2,
+        int(has_c2p),
+        int(has_p2c),
+        _lib.DTYPE_CODES[qkv.dtype],
+        int(strict_fp32),
+        _lib.current_stream_handle(qkv.device),
+    )
+    _lib.check(code, "dflash_attention_rel_fwd")
+    return out
+
+
+@deberta_attention_rel.register_fake
+def _deberta_attention_rel_fake(qkv, pos_key, pos_query, delta_to_local, attention_mask,
+                                num_heads, head_dim, score_scale_log2, has_c2p, has_p2c,
+                                strict_fp32):
+    batch, length, _ = qkv.shape
+    return qkv.new_empty((batch, length, num_heads * head_dim))
+
+
+def _require_2d_padding_mask(
+    attention_mask: torch.Tensor, batch_size: int, sequence_length: int
+) -> torch.Tensor:
+    """Validate the factorized ``[B, L]`` padding mask (``kernel.py:441-458``)."""
+
+    if attention_mask.dim() != 2:
+        raise ValueError(
+            "the HIP fast path requires a factorized padding mask with shape "
+            "[B, L]; arbitrary pairwise masks are not supported"
+        )
+    if attention_mask.shape != (batch_size, sequence_length):
+        raise ValueError(
+            f"attention_mask shape {tuple(attention_mask.shape)} does not match "
+            f"[{batch_size}, {sequence_length}]"
+        )
+    return attention_mask.bool().contiguous()
+
+
+class HipPreparedPositionPlan(NamedTuple):
+    """Layer projections plus one shared compact position LUT (``kernel.py:461-468``)."""
+
+    sequence_length: int
+    active_slots: torch.Tensor
+    delta_to_local: torch.Tensor
+    pos_key: torch.Tensor | None
+    pos_query: torch.Tensor | None
+    windowed: bool = True
+
+
+def lut_is_window_safe(delta_to_local: torch.Tensor) -> bool:
+    """True if the LUT steps by 0 or 1 per delta, the fused kernel's precondition.
+
+    Every plan built from a monotone bucket function satisfies it; a plan that
+    does not is run through the table path instead.
+    """
+
+    if delta_to_local.numel() < 2:
+        return True
+    step = delta_to_local.diff()
+    return bool(((step >= 0) & (step <= 1)).all())
+
+
+class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttention):
+    """Forward-only MI355X DeBERTa-v2/v3 self-attention.
+
+    Head dimensions 32, 64 and 128; fp16, bf16 and fp32.  gfx950 has no TF32
+    matrix path, so ``fp32_precision="fast"`` is accepted for API parity and
+    runs the same IEEE fp32 MFMA as ``"strict"``.
+
+    ``relative_mode="fused"`` (default) computes the c2p/p2c scores inside the
+    attention kernel; ``"table"`` reproduces the reference's data flow (two
+    separate score GEMMs, then the fused kernel reading ``[B, H, L, S]`` tables).
+    """
+
+    def __init__(
+        self,
+        config: DebertaAttentionConfig | Any,
+        *,
+        position_plan_cache: SharedPositionPlanCache | None = None,
+        fp32_precision: str = "strict",
+        relative_mode: str = "fused",
+    ) -> None:
+        super().__init__(config, position_plan_cache=position_plan_cache)
+        if fp32_precision not in {"strict", "fast"}:
+            raise ValueError("fp32_precision must be 'strict' or 'fast'")
+        if relative_mode not in RELATIVE_MODES:
+            raise ValueError(f"relative_mode must be one of {RELATIVE_MODES}")
+        self.fp32_precision = fp32_precision
+        self.relative_mode = relative_mode
+        self._hip_position_projection_cache: dict[tuple[int, str], HipPreparedPositionPlan] = {}
+
+    def clear_inference_cache(self) -> None:
+        super().clear_inference_cache()
+        if hasattr(self, "_hip_position_projection_cache"):
+            self._hip_position_projection_cache.clear()
+
+    @torch.no_grad()
+    def prepare_shape(
+        self, sequence_length: int, device: torch.device | str | None = None
+    ) -> HipPreparedPositionPlan:
+        """Prepare the ``O(L)`` plan: LUT plus the active rows of the projected table."""
+
+        if self.training:
+            raise RuntimeError("prepare_shape() requires module.eval()")
+        resolved = canonical_device(device, self._plan_device())
+        if resolved.type != "cuda":
+            raise ValueError("HIP shape plans must be prepared on a GPU device")
+        key = (sequence_length, str(resolved))
+        hit = self._hip_position_projection_cache.get(key)
+        if hit is not None:
+            return hit
+        indices = self.position_plan_cache.compact(sequence_length, resolved)
+        pos_key, pos_query = self._project_active_positions(indices.active_slots)
+        lut = indices.delta_to_local.to(dtype=torch.int32).contiguous()
+        plan = HipPreparedPositionPlan(
+            sequence_length=sequence_length,
+            active_slots=indices.active_slots,
+            delta_to_local=lut,
+            pos_key=pos_key,
+            pos_query=pos_query,
+            windowed=lut_is_window_safe(lut),
+        )
+        self._hip_position_projection_cache[key] = plan
+        return plan
+
+    def _validate_hip_call(self, hidden_states: torch.Tensor) -> None:
+        if hidden_states.device.type != "cuda":
+            raise RuntimeError("HipInferenceDisentangledSelfAttention requires a GPU tensor")
+        if hidden_states.dtype not in SUPPORTED_DTYPES:
+            raise TypeError("the HIP path supports FP16, BF16, and FP32")
+        if self.attention_head_size not in SUPPORTED_HEAD_DIMS:
+            raise ValueError("the HIP path supports attention head dimensions 32, 64, and 128")
+        self._validate_inference_call()
+        _lib.load()
+
+    def score_scale_log2(self) -> float:
+        return LOG2E / self._scale(self.scale_factor)
+
+    def forward_prepared(
+        self,
+        hidden_states: torch.Tensor,
+        attention_mask: torch.Tensor,
+        plan: HipPreparedPositionPlan,
+    ) -> tuple[torch.Tensor, None]:
+        """Fused forward using a plan prepared outside the hot path (``kernel.py:545-608``)."""
+
+        self._validate_hip_call(hidden_states)
+        batch, length = hidden_states.shape[:2]
+        if length != plan.sequence_length:
+            raise ValueError(
+                f"prepared length {plan.sequence_length} does not match input length {length}"
+            )
+        mask = _require_2d_padding_mask(attention_mask, batch, length)
+        has_c2p, has_p2c = self.has_c2p, self.has_p2c
+        if has_c2p and plan.pos_key is None:
+            raise ValueError("prepared HIP plan has no content-to-position keys")
+        if has_p2c and plan.pos_query is None:
+            raise ValueError("prepared HIP plan has no position-to-content queries")
+        if self._cached_qkv_weight is None:
+            raise RuntimeError(
+                "fused QKV projection is not prepared; call prepare_for_inference() first"
+            )
+        scale_log2 = self.score_scale_log2()
+        strict = self.fp32_precision == "strict"
+        fused = F.linear(hidden_states, self._cached_qkv_weight, self._cached_qkv_bias)
+        if fused.stride(-1) != 1 or fused.stride(1) != fused.size(-1):
+            fused = fused.contiguous()
+        if self.relative_mode == "fused" and plan.windowed:
+            placeholder = plan.delta_to_local
+            output = deberta_attention_rel(
+                fused,
+                plan.pos_key if has_c2p else placeholder,
+                plan.pos_query if has_p2c else placeholder,
+                plan.delta_to_local,
+                mask,
+                self.num_attention_heads,
+                self.attention_head_size,
+                scale_log2,
+                has_c2p,
+                has_p2c,
+                strict,
+            )
+            return output, None
+
+        query, key, value = fused.split(self.all_head_size, dim=-1)
+        q = self._reshape_heads(query, batch, length)
+        k = self._reshape_heads(key, batch, length)
+        v = self._reshape_heads(value, batch, length)
+        c2p = torch.matmul(q, plan.pos_key.transpose(-1, -2)) if has_c2p else q
+        p2c = torch.matmul(k, plan.pos_query.transpose(-1, -2)) if has_p2c else k
+        output = deberta_attention(
+            q,
+            k,
+            v,
+            c2p,
+            p2c,
+            plan.delta_to_local,
+            mask,
+            self.num_attention_heads,
+            length,
+            plan.active_slots.numel(),
+            scale_log2,
+            has_c2p,
+            has_p2c,
+            hidden_states.dtype == torch.bfloat16,
+            hidden_states.dtype == torch.float32,
+            strict,
+        )
+        return output, None
+
+    def forward(
+        self,
+        hidden_states: torch.Tensor,
+        attention_mask: torch.Tensor,
+        output_attentions: bool = False,
+        query_states: torch.Tensor | None = None,
+        relative_pos: torch.Tensor | None = None,
+        rel_embeddings: torch.Tensor | None = None,
+    ) -> tuple[torch.Tensor, None]:
+        """HF-signature wrapper with lazy preparation (``kernel.py:610-638``)."""
+
+        self._validate_hip_call(hidden_states)
+        if output_attentions:
+            raise ValueError("output_attentions=True is not supported by the HIP path")
+        if query_states is not None:
+            raise ValueError("the HIP path supports self-attention only")
+        if relative_pos is not None:
+            raise ValueError("custom relative_pos tensors are not supported by the HIP path")
+        self._lazy_prepare(rel_embeddings)
+        plan = self.prepare_shape(hidden_states.size(1), hidden_states.device)
+        return self.forward_prepared(hidden_states, attention_mask, plan)
+
+
+DisentangledFlashAttention = HipInferenceDisentangledSelfAttention
+
+
+def attention_flops(batch: int, heads: int, length: int, head_dim: int) -> int:
+    """Headline FLOPs of QK^T + PV over the dense length (FlashAttention convention)."""
+
+    return 4 * batch * heads * length * length * head_dim
+
+
+def relative_flops(batch: int, heads: int, length: int, head_dim: int, slots: int,
+                   modes: int = 2) -> int:
+    """FLOPs of the c2p/p2c score products over the active slots."""
+
+    return 2 * modes * batch * heads * length * slots * head_dim
+
+
+__all__ = [
+    "DisentangledFlashAttention",
+    "HipInferenceDisentangledSelfAttention",
+    "HipPreparedPositionPlan",
+    "attention_flops",
+    "deberta_attention",
+    "deberta_attention_rel",
+    "relative_flops",
+]

@@ -1,0 +1,100 @@
+/*
+ * dflash.h - C ABI of the MI355X (gfx950) DeBERTa disentangled-attention library.
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer to
+ * memory the caller owns; the library allocates nothing and launches on the
+ * HIP stream it is given (NULL = the default stream).  Calls are asynchronous
+ * with respect to the host, like the kernel launch they replace.
+ *
+ * Return value: 0 on success, a negative DFLASH_ERR_* code for an argument
+ * error detected on the host (nothing is launched), or a positive hipError_t
+ * from the launch.  dflash_error_string() turns either into text.
+ *
+ * dtype codes: 0 = fp16, 1 = bf16, 2 = fp32.  Head dimension D is 32, 64 or 128.
+ */
+#ifndef DFLASH_H_
+#define DFLASH_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFLASH_API __attribute__((visibility("default")))
+
+#define DFLASH_ABI_VERSION 1
+
+#define DFLASH_DTYPE_FP16 0
+#define DFLASH_DTYPE_BF16 1
+#define DFLASH_DTYPE_FP32 2
+
+#define DFLASH_OK 0
+#define DFLASH_ERR_NULL (-1)
+#define DFLASH_ERR_SHAPE (-2)
+#define DFLASH_ERR_HEAD_DIM (-3)
+#define DFLASH_ERR_DTYPE (-4)
+#define DFLASH_ERR_ALIGN (-5)
+#define DFLASH_ERR_TOO_LARGE (-6)
+
+/*
+ * Fused attention over precomputed relative-score tables.
+ *
+ * Replaces the reference op torch.ops.gliner2_attention.deberta_attention
+ * (/root/reference/src/disentangled_flash/kernel.py:368-438, kernel body
+ * kernel.py:137-345) argument for argument:
+ *   query, key, value : [B, H, L, D] contiguous, dtype `dtype`
+ *   c2p, p2c          : [B, H, L, S] contiguous, unscaled Q.Kr^T / K.Qr^T over
+ *                       the active slots; ignored (may be NULL) when the mode is off
+ *   delta_to_local    : int32 [2L-1], local slot of delta i-j at index i-j+L-1
+ *   attention_mask    : uint8 [B, L], nonzero = kept token (the reference's bool mask)
+ *   out               : [B, L, H*D], dtype `dtype`
+ *   score_scale_log2  : log2(e) / sqrt(D * (1 + has_c2p + has_p2c))  (kernel.py:587-588)
+ *   strict_fp32       : accepted for signature parity; gfx950 has no TF32 MFMA,
+ *                       so fp32 always runs IEEE fp32 MFMA.
+ */
+DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const void* value,
+                         const void* c2p, const void* p2c, const int32_t* delta_to_local,
+                         const uint8_t* attention_mask, void* out, int B, int H, int L, int D,
+                         int S, float score_scale_log2, int has_c2p, int has_p2c, int dtype,
+                         int strict_fp32, void* stream);
+
+/*
+ * Fused attention computing the relative scores inside the kernel.
+ *
+ * Same output contract as dflash_attention_fwd, but it takes the projected
+ * active relative rows instead of the [B, H, L, S] tables, so the separate
+ * C2P/P2C GEMMs of the reference's forward_prepared
+ * (/root/reference/src/disentangled_flash/kernel.py:574-585) and their
+ * 2 x B*H*L*S HBM round trip disappear:
+ *   query/key/value   : element (b, h, i, :) at base + b*stride_b + h*stride_h + i*stride_l,
+ *                       D contiguous elements; strides in elements, 16-byte aligned.
+ *                       Pass the three column blocks of the fused QKV projection
+ *                       output [B, L, 3*H*D] directly (stride_b = 3*H*D*L,
+ *                       stride_h = D, stride_l = 3*H*D) - no head reshape copy.
+ *   pos_key, pos_query: [H, S, D] contiguous, the plan's pos_key / pos_query
+ *                       (kernel.py:461-468, 522-523)
+ *   delta_to_local    : as above, and additionally non-decreasing with steps of
+ *                       0 or 1 (true for every plan built from a monotone bucket
+ *                       function; see position.py:89-128).  The kernel relies on
+ *                       it to map a tile's deltas to a contiguous slot window.
+ */
+DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,
+                             int64_t stride_b, int64_t stride_h, int64_t stride_l,
+                             const void* pos_key, const void* pos_query,
+                             const int32_t* delta_to_local, const uint8_t* attention_mask,
+                             void* out, int B, int H, int L, int D, int S,
+                             float score_scale_log2, int has_c2p, int has_p2c, int dtype,
+                             int strict_fp32, void* stream);
+
+/* Text for a return code of any dflash_* entry point. */
+DFLASH_API const char* dflash_error_string(int code);
+
+/* DFLASH_ABI_VERSION of the loaded library. */
+DFLASH_API int dflash_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFLASH_H_ */

@@ -1,0 +1,208 @@
+"""Parity of the HIP attention kernels (through the C ABI) with the float64 reference.
+
+Tolerances (max-abs on the attention output): fp16 2e-3, bf16 1e-2, fp32 1e-5.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from gpu_reference import fused_reference
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5}
+LOG2E = 1.4426950408889634
+
+
+def _lut(length: int, device):
+    from disentangled_flash.position import compact_position_plan
+
+    active, lut = compact_position_plan(length, position_buckets=256, max_relative_positions=512,
+                                        position_embedding_size=256)
+    return active.numel(), lut.to(device)
+
+
+def _mask(batch: int, length: int, pattern: str, gen: torch.Generator):
+    mask = torch.ones(batch, length, dtype=torch.bool)
+    if pattern in ("right", "left"):
+        low = max(1, length // 3)
+        lengths = torch.randint(low, length + 1, (batch,), generator=gen)
+        pos = torch.arange(length)[None]
+        mask = pos < lengths[:, None] if pattern == "right" else pos >= length - lengths[:, None]
+    elif pattern == "heavy":
+        mask[:, max(1, length // 4):] = False
+    elif pattern == "all":
+        mask[:] = False
+    elif pattern == "boundary":
+        choices = torch.tensor([1, 63, 64, 65, 127, 129, 383, 384, 511, 512])
+        lens = choices[torch.arange(batch) % len(choices)].clamp(max=length)
+        mask = torch.arange(length)[None] < lens[:, None]
+    return mask
+
+
+def _inputs(batch, heads, length, dim, dtype, pattern, seed, scale_qk=1.0):
+    gen = torch.Generator().manual_seed(seed)
+    s, lut = _lut(length, "cuda")
+    q, k, v = (torch.randn(batch, heads, length, dim, generator=gen) for _ in range(3))
+    pos_key = torch.randn(heads, s, dim, generator=gen)
+    pos_query = torch.randn(heads, s, dim, generator=gen)
+    q, k = q * scale_qk, k * scale_qk
+    tensors = [t.to("cuda", dtype) for t in (q, k, v, pos_key, pos_query)]
+    return (*tensors, lut, _mask(batch, length, pattern, gen).cuda())
+
+
+def _fused_qkv(q, k, v):
+    b, h, length, d = q.shape
+    flat = [t.permute(0, 2, 1, 3).reshape(b, length, h * d) for t in (q, k, v)]
+    return torch.cat(flat, dim=-1).contiguous()
+
+
+def _run_rel(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c):
+    from disentangled_flash.kernel import deberta_attention_rel
+
+    d = q.shape[-1]
+    factor = 1 + int(has_c2p) + int(has_p2c)
+    scale_log2 = LOG2E / math.sqrt(d * factor)
+    out = deberta_attention_rel(_fused_qkv(q, k, v), pos_key, pos_query, lut, mask,
+                                q.shape[1], d, scale_log2, has_c2p, has_p2c, True)
+    torch.cuda.synchronize()
+    return out
+
+
+def _run_table(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c):
+    from disentangled_flash.kernel import deberta_attention
+
+    b, h, length, d = q.shape
+    factor = 1 + int(has_c2p) + int(has_p2c)
+    c2p = torch.matmul(q, pos_key.transpose(-1, -2)) if has_c2p else q
+    p2c = torch.matmul(k, pos_query.transpose(-1, -2)) if has_p2c else k
+    out = deberta_attention(q.contiguous(), k.contiguous(), v.contiguous(), c2p, p2c, lut, mask,
+                            h, length, pos_key.shape[1], LOG2E / math.sqrt(d * factor),
+                            has_c2p, has_p2c, q.dtype == torch.bfloat16, q.dtype == torch.float32,
+                            True)
+    torch.cuda.synchronize()
+    return out
+
+
+def _check(out, q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c, label):
+    d = q.shape[-1]
+    factor = 1 + int(has_c2p) + int(has_p2c)
+    rounding = None if q.dtype == torch.float32 else q.dtype
+    ref = fused_reference(q, k, v, pos_key, pos_query, lut, mask, math.sqrt(d * factor),
+                          has_c2p, has_p2c, round_tables_to=rounding)
+    err = (out.double() - ref).abs().max().item()
+    assert torch.isfinite(out).all(), f"{label}: non-finite output"
+    assert err <= TOL[q.dtype], f"{label}: max abs err {err:.3e} > {TOL[q.dtype]:.0e}"
+    return err
+
+
+MODES = {"both": (True, True), "c2p": (True, False), "p2c": (False, True), "none": (False, False)}
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("dim,heads", [(32, 4), (64, 3), (128, 2)])
+@pytest.mark.parametrize("mode", list(MODES))
+def test_rel_kernel_modes_and_head_dims(dtype, dim, heads, mode):
+    has_c2p, has_p2c = MODES[mode]
+    args = _inputs(2, heads, 200, dim, DTYPES[dtype], "right", seed=dim + heads)
+    out = _run_rel(*args, has_c2p, has_p2c)
+    print(f"rel {dtype} d={dim} {mode}: err={_check(out, *args, has_c2p, has_p2c, 'rel'):.2e}")
+
+
+@pytest.mark.parametrize("length", [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257,
+                                    511, 512, 513, 1024])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_rel_kernel_boundary_lengths(length, dtype):
+    args = _inputs(2, 2, length, 64, DTYPES[dtype], "right", seed=length)
+    out = _run_rel(*args, True, True)
+    _check(out, *args, True, True, f"L={length}")
+
+
+@pytest.mark.parametrize("pattern", ["none", "right", "left", "heavy", "all", "boundary"])
+@pytest.mark.parametrize("dtype", list(DTYPES))
+def test_rel_kernel_mask_patterns(pattern, dtype):
+    args = _inputs(10, 2, 384, 64, DTYPES[dtype], pattern, seed=11)
+    out = _run_rel(*args, True, True)
+    _check(out, *args, True, True, pattern)
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("mode", ["both", "c2p", "p2c", "none"])
+def test_table_kernel_matches_reference(dtype, mode):
+    has_c2p, has_p2c = MODES[mode]
+    args = _inputs(3, 2, 300, 64, DTYPES[dtype], "left", seed=5)
+    out = _run_table(*args, has_c2p, has_p2c)
+    _check(out, *args, has_c2p, has_p2c, "table")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("pattern", ["right", "none"])
+def test_c2_full_size(dtype, pattern):
+    """B=32, L=512, H=12, d=64, Q/K/V/Qr/Kr ~ N(0,1)/sqrt(d)."""
+
+    gen = torch.Generator().manual_seed(2024)
+    b, h, length, d = 32, 12, 512, 64
+    s, lut = _lut(length, "cuda")
+    assert s == 511
+    scale = 1.0 / math.sqrt(d)
+    q, k, v = (torch.randn(b, h, length, d, generator=gen) * scale for _ in range(3))
+    pos_key, pos_query = (torch.randn(h, s, d, generator=gen) * scale for _ in range(2))
+    if pattern == "right":
+        lengths = torch.randint(256, 513, (b,), generator=gen)
+        mask = torch.arange(length)[None] < lengths[:, None]
+    else:
+        mask = torch.ones(b, length, dtype=torch.bool)
+    args = [t.to("cuda", DTYPES[dtype]) for t in (q, k, v, pos_key, pos_query)] + [lut, mask.cuda()]
+    out = _run_rel(*args, True, True)
+    d64 = [t.double() for t in args[:5]]
+    ref = fused_reference(*d64, lut, args[6], math.sqrt(3 * d), True, True)
+    err = (out.double() - ref).abs().max().item()
+    assert err <= TOL[DTYPES[dtype]], f"C2 {dtype} {pattern}: {err:.3e}"
+    table = _run_table(*args, True, True)
+    assert (table.double() - ref).abs().max().item() <= TOL[DTYPES[dtype]]
+
+
+def test_rel_and_table_agree_fp32():
+    args = _inputs(2, 3, 257, 64, torch.float32, "right", seed=9)
+    a = _run_rel(*args, True, True)
+    b = _run_table(*args, True, True)
+    assert (a - b).abs().max().item() <= 2e-6
+
+
+def test_rel_kernel_reads_strided_qkv_without_copies():
+    """The fused op consumes the [B, L, 3*H*d] projection output in place."""
+
+    from disentangled_flash.kernel import deberta_attention_rel
+
+    args = _inputs(2, 4, 96, 64, torch.float16, "right", seed=3)
+    q, k, v, pos_key, pos_query, lut, mask = args
+    qkv = _fused_qkv(q, k, v)
+    out = deberta_attention_rel(qkv, pos_key, pos_query, lut, mask, 4, 64,
+                                LOG2E / math.sqrt(192), True, True, True)
+    torch.cuda.synchronize()
+    _check(out, *args, True, True, "strided")
+
+
+def test_c_abi_rejects_bad_arguments():
+    from disentangled_flash import _lib
+
+    lib = _lib.load()
+    x = torch.zeros(16, device="cuda", dtype=torch.float16)
+    rc = lib.dflash_attention_fwd(x.data_ptr(), x.data_ptr(), x.data_ptr(), None, None,
+                                  None, x.data_ptr(), x.data_ptr(), 1, 1, 1, 48, 1, 1.0,
+                                  0, 0, 0, 1, None)
+    assert rc == -3
+    rc = lib.dflash_attention_fwd(x.data_ptr(), x.data_ptr(), x.data_ptr(), None, None,
+                                  None, x.data_ptr(), x.data_ptr(), 1, 1, 1, 64, 1, 1.0,
+                                  0, 0, 7, 1, None)
+    assert rc == -4
+    rc = lib.dflash_attention_fwd(x.data_ptr(), x.data_ptr(), x.data_ptr(), None, None,
+                                  None, x.data_ptr(), x.data_ptr(), 1, 1, 1, 64, 1, 1.0,
+                                  1, 0, 0, 1, None)
+    assert rc == -1
+    assert b"head dimension" in lib.dflash_error_string(-3)
