@@ -1,0 +1,393 @@
+"""Benchmark of the fused DeBERTa disentangled-attention hot path on one MI355X.
+
+Headline (BASELINE.json ``metric``): fused attention TFLOP/s and fraction of the
+fp16 dense MFMA peak at the attention microbench configuration
+(B=32, L=512, H=12, d=64, c2p|p2c, position_buckets=256, max_rel=512), plus the
+12-layer encoder latency at B=32, L=512 fp16 for the ``hip`` and the torch
+``optimized`` backends on the same GPU.
+
+A step is one launch of the fused attention over the whole batch with Q/K/V,
+the projected relative rows, the LUT and the mask already resident in HBM.
+``value`` counts F_attn = 4*B*H*L^2*d (QK^T + PV over the dense L) per step.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-encoder] [--skip-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for entry in (str(REPO / "disentangled-flash_amd"), str(REPO)):
+    if entry not in sys.path:
+        sys.path.insert(0, entry)
+
+import torch  # noqa: E402
+
+PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3}
+HBM_PEAK_GBS = 8000.0
+LOG2E = 1.4426950408889634
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+TRAFFIC_FILE = REPO / "profiles" / "attention_c2_fp16_traffic.json"
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def c2_inputs(dtype: torch.dtype, padded: bool, seed: int = 2024, batch: int = 32,
+              heads: int = 12, length: int = 512, dim: int = 64, device: str = "cuda"):
+    """Q/K/V and Qr/Kr ~ N(0,1)/sqrt(d); lengths U[256, 512] or none."""
+
+    from disentangled_flash.position import compact_position_plan
+
+    active, lut = compact_position_plan(length, position_buckets=256, max_relative_positions=512,
+                                        position_embedding_size=256)
+    gen = torch.Generator().manual_seed(seed)
+    scale = 1.0 / math.sqrt(dim)
+    q, k, v = (torch.randn(batch, heads, length, dim, generator=gen) * scale for _ in range(3))
+    pos_key, pos_query = (torch.randn(heads, active.numel(), dim, generator=gen) * scale
+                          for _ in range(2))
+    if padded:
+        lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen)
+        mask = torch.arange(length)[None] < lengths[:, None]
+    else:
+        mask = torch.ones(batch, length, dtype=torch.bool)
+    qkv = torch.cat([t.permute(0, 2, 1, 3).reshape(batch, length, heads * dim) for t in (q, k, v)],
+                    dim=-1)
+    to = lambda t: t.to(device, dtype).contiguous()  # noqa: E731
+    return {
+        "qkv": to(qkv), "q": to(q), "k": to(k), "v": to(v),
+        "pos_key": to(pos_key), "pos_query": to(pos_query),
+        "lut": lut.to(device), "mask": mask.to(device),
+        "batch": batch, "heads": heads, "length": length, "dim": dim,
+        "slots": active.numel(), "valid_fraction": float(mask.float().mean()),
+    }
+
+
+def time_launches(fn, steps: int, warmup: int) -> float:
+    """Average milliseconds per call over ``steps`` back-to-back calls (HIP events)."""
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_p50(fn, steps: int, warmup: int) -> float:
+    """Median milliseconds of individually event-timed calls."""
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(steps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        samples.append(start.elapsed_time(end))
+    return statistics.median(samples)
+
+
+def fused_call(inp):
+    from disentangled_flash.kernel import deberta_attention_rel
+
+    scale_log2 = LOG2E / math.sqrt(3 * inp["dim"])
+    return lambda: deberta_attention_rel(inp["qkv"], inp["pos_key"], inp["pos_query"], inp["lut"],
+                                         inp["mask"], inp["heads"], inp["dim"], scale_log2,
+                                         True, True, True)
+
+
+def table_call(inp):
+    """Reference data flow: two separate score GEMMs, then the table-reading kernel."""
+
+    from disentangled_flash.kernel import deberta_attention
+
+    scale_log2 = LOG2E / math.sqrt(3 * inp["dim"])
+
+    def run():
+        c2p = torch.matmul(inp["q"], inp["pos_key"].transpose(-1, -2))
+        p2c = torch.matmul(inp["k"], inp["pos_query"].transpose(-1, -2))
+        return deberta_attention(inp["q"], inp["k"], inp["v"], c2p, p2c, inp["lut"], inp["mask"],
+                                 inp["heads"], inp["length"], inp["slots"], scale_log2,
+                                 True, True, inp["q"].dtype == torch.bfloat16,
+                                 inp["q"].dtype == torch.float32, True)
+
+    return run
+
+
+def torch_optimized_call(inp):
+    """The prepared torch equation (``_torch.py:339-387``) on the GPU from resident Q/K/V."""
+
+    from disentangled_flash.position import SharedPositionPlanCache
+
+    cache = SharedPositionPlanCache(position_buckets=256, max_relative_positions=512,
+                                    position_embedding_size=256)
+    pair = cache.dense(inp["length"], inp["q"].device).pair_to_local
+    b, h, length = inp["batch"], inp["heads"], inp["length"]
+    scale = math.sqrt(3 * inp["dim"])
+    q, k, v = inp["q"], inp["k"], inp["v"]
+    mask = inp["mask"]
+
+    def run():
+        index = pair.expand(b, h, length, length)
+        scores = torch.matmul(q, k.transpose(-1, -2) / scale)
+        scores = scores + torch.gather(torch.matmul(q, inp["pos_key"].transpose(-1, -2)) / scale,
+                                       -1, index)
+        raw = torch.matmul(k, inp["pos_query"].transpose(-1, -2)) / scale
+        scores = scores + torch.gather(raw.transpose(-1, -2), -2, index)
+        pairm = mask[:, None, None, :] & mask[:, None, :, None]
+        scores = scores.masked_fill(~pairm, torch.finfo(q.dtype).min)
+        ctx = torch.matmul(torch.softmax(scores, dim=-1), v)
+        return ctx.permute(0, 2, 1, 3).reshape(b, length, h * inp["dim"])
+
+    return run
+
+
+def attention_flops(inp) -> float:
+    return 4.0 * inp["batch"] * inp["heads"] * inp["length"] ** 2 * inp["dim"]
+
+
+def relative_flops(inp) -> float:
+    return 4.0 * inp["batch"] * inp["heads"] * inp["length"] * inp["slots"] * inp["dim"]
+
+
+def algorithmic_bytes(inp) -> float:
+    """HBM bytes a fused launch must move: Q, K, V, O, the relative rows, LUT and mask."""
+
+    esize = inp["qkv"].element_size()
+    per_tensor = inp["batch"] * inp["heads"] * inp["length"] * inp["dim"] * esize
+    rel = 2 * inp["heads"] * inp["slots"] * inp["dim"] * esize
+    return 4 * per_tensor + rel + inp["lut"].numel() * 4 + inp["mask"].numel()
+
+
+def encoder_config():
+    from transformers import DebertaV2Config
+
+    return DebertaV2Config(
+        vocab_size=128100, hidden_size=768, num_hidden_layers=12, num_attention_heads=12,
+        intermediate_size=3072, hidden_act="gelu", hidden_dropout_prob=0.0,
+        attention_probs_dropout_prob=0.0, max_position_embeddings=512, type_vocab_size=0,
+        initializer_range=0.02, layer_norm_eps=1e-7, relative_attention=True,
+        max_relative_positions=-1, position_buckets=256, pos_att_type=["p2c", "c2p"],
+        norm_rel_ebd="layer_norm", share_att_key=True, conv_kernel_size=3, conv_act="gelu",
+        position_biased_input=False,
+    )
+
+
+def encoder_inputs(batch: int, length: int, dtype, device, seed: int = 19):
+    """Embedding-table hidden states and U[L/2, L] right-padded masks (C3)."""
+
+    gen = torch.Generator().manual_seed(seed)
+    table = torch.randn(128100, 768, generator=gen) * 0.02
+    table[0].zero_()
+    tokens = torch.randint(1, 128100, (batch, length), generator=gen)
+    lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen)
+    mask = torch.arange(length)[None] < lengths[:, None]
+    tokens = tokens.masked_fill(~mask, 0)
+    hidden = table[tokens].to(device=device, dtype=dtype).contiguous()
+    # Integer mask, as a tokenizer produces it (Hugging Face's ConvLayer computes 1 - mask).
+    return hidden, mask.to(device=device, dtype=torch.long)
+
+
+def bench_encoder(batch: int, length: int, steps: int, warmup: int):
+    """12-layer encoder latency: HF original vs torch ``optimized`` vs ``hip``."""
+
+    import copy
+
+    from transformers import DebertaV2Model
+
+    from disentangled_flash import enable_deberta_inference
+
+    torch.manual_seed(17)
+    base = DebertaV2Model(encoder_config()).to("cuda", torch.float16).eval()
+    hidden, mask = encoder_inputs(batch, length, torch.float16, "cuda")
+    results = {}
+    with torch.inference_mode():
+        original = base.encoder
+        results["original_ms"] = time_p50(
+            lambda: original(hidden, mask, output_hidden_states=False), steps, warmup)
+        reference_out = original(hidden, mask, output_hidden_states=False).last_hidden_state
+        for backend in ("optimized", "hip"):
+            model = copy.deepcopy(base)
+            enable_deberta_inference(model, backend=backend, sequence_lengths=[length])
+            encoder = model.encoder
+            plans = encoder._active_plans
+            run = lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: E731
+                                                   output_hidden_states=False)
+            results[f"{backend}_ms"] = time_p50(run, steps, warmup)
+            out = run().last_hidden_state
+            results[f"{backend}_max_abs_err_vs_original"] = float(
+                (out.float() - reference_out.float()).abs().max())
+            del model, encoder
+            torch.cuda.empty_cache()
+    results["speedup_vs_optimized"] = results["optimized_ms"] / results["hip_ms"]
+    results["speedup_vs_original"] = results["original_ms"] / results["hip_ms"]
+    return results
+
+
+def cpu_baseline(target_seconds: float = 12.0):
+    """Oracle restatement of the ``optimized`` equation, fp32, on the host CPU.
+
+    Bounded sample of the C2 workload: one sequence (B=1 of 32) at L=512, H=12,
+    d=64 per call, repeated for about ``target_seconds``; reported in the same
+    unit (F_attn TFLOP/s).
+    """
+
+    from oracle.optimized import optimized_core
+    from oracle.positions import compact_plan, dense_map
+
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    inp = c2_inputs(torch.float32, padded=True, batch=1, device="cpu")
+    pair = torch.from_numpy(dense_map(compact_plan(512, position_buckets=256,
+                                                   max_relative_positions=512,
+                                                   position_embedding_size=256)[1], 512))
+    args = (inp["q"], inp["k"], inp["v"], inp["pos_key"], inp["pos_query"], pair, inp["mask"],
+            math.sqrt(192))
+    for _ in range(2):
+        optimized_core(*args)
+    calls = 0
+    start = time.perf_counter()
+    samples = []
+    while time.perf_counter() - start < target_seconds:
+        t0 = time.perf_counter()
+        optimized_core(*args)
+        samples.append(time.perf_counter() - t0)
+        calls += 1
+    median = statistics.median(samples)
+    return {
+        "value": attention_flops(inp) / median / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle/optimized.py optimized_core, fp32, B=1 of the B=32 C2 batch "
+                   f"(L=512 H=12 d=64, padded), {calls} calls in {sum(samples):.1f}s, "
+                   f"median {median * 1e3:.1f} ms/call"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--encoder-steps", type=int, default=20)
+    parser.add_argument("--skip-encoder", action="store_true")
+    parser.add_argument("--skip-cpu", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
+              "(see DESIGN.md for how the attention shards across GPUs); use --gpus 1.",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+
+    from disentangled_flash import _lib
+
+    _lib.load()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    # ---- headline: fused fp16 attention, C2 without padding (every FLOP real) ----
+    full = c2_inputs(torch.float16, padded=False)
+    f_attn = attention_flops(full)
+    f_rel = relative_flops(full)
+    ms = time_launches(fused_call(full), args.steps, args.warmup)
+    tflops = f_attn / (ms * 1e-3) / 1e12
+    log(f"fused fp16 unpadded: {ms * 1e3:.1f} us  {tflops:.1f} TFLOP/s (F_attn)")
+
+    extra = {}
+    padded = c2_inputs(torch.float16, padded=True)
+    ms_pad = time_launches(fused_call(padded), args.steps, args.warmup)
+    extra["fp16_padded"] = {"us": ms_pad * 1e3, "tflops_f_attn": f_attn / ms_pad / 1e9,
+                            "valid_fraction": padded["valid_fraction"]}
+    for name in ("bf16",):
+        inp = c2_inputs(DTYPES[name], padded=False)
+        t = time_launches(fused_call(inp), args.steps, args.warmup)
+        extra[f"{name}_unpadded"] = {"us": t * 1e3, "tflops_f_attn": f_attn / t / 1e9}
+        del inp
+    t_table = time_launches(table_call(full), max(5, args.steps // 5), 3)
+    extra["reference_dataflow_fp16_us"] = t_table * 1e3
+    t_torch = time_launches(torch_optimized_call(full), max(5, args.steps // 5), 2)
+    extra["torch_optimized_attention_fp16_us"] = t_torch * 1e3
+    extra["speedup_vs_torch_optimized_attention"] = t_torch / ms
+    log(f"table data flow {t_table * 1e3:.1f} us, torch optimized {t_torch * 1e3:.1f} us")
+    del padded
+    torch.cuda.empty_cache()
+
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": "fused attn TFLOP/s (% MFMA peak) + 12-layer encoder ms, B=32 L=512 fp16",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": "attention microbench (BASELINE configs[1]): fused disentangled attention, "
+                        "c2p|p2c, no padding; F_attn = 4*B*H*L^2*d numerator",
+            "batch": full["batch"], "seq_len": full["length"], "heads": full["heads"],
+            "head_dim": full["dim"], "active_slots": full["slots"], "position_buckets": 256,
+            "max_relative_positions": 512, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_TFLOPS["fp16"],
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_TFLOPS["fp16"], 4),
+            "traffic": traffic,
+            "f_total_tflops": round((f_attn + f_rel) / (ms * 1e-3) / 1e12, 2),
+            "f_total_frac": round((f_attn + f_rel) / (ms * 1e-3) / 1e12 / PEAK_TFLOPS["fp16"], 4),
+            "algorithmic_bytes": algorithmic_bytes(full),
+            "algorithmic_gbs": round(algorithmic_bytes(full) / (ms * 1e-3) / 1e9, 1),
+        },
+        "extra": extra,
+    }
+    del full
+    torch.cuda.empty_cache()
+
+    if not args.skip_encoder:
+        enc = bench_encoder(32, 512, args.encoder_steps, 3)
+        line["encoder"] = {"batch": 32, "seq_len": 512, "layers": 12, "dtype": "fp16",
+                           **{k: (round(v, 4) if isinstance(v, float) else v)
+                              for k, v in enc.items()}}
+        log(f"encoder: {enc}")
+    if not args.skip_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+        log(f"cpu baseline: {line['cpu_baseline']}")
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -43,10 +43,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;               // wavefronts per workgroup
-constexpr int kQueriesPerWave = 32;     // query rows owned by one wavefront
-constexpr int kBlockM = kWaves * kQueriesPerWave;
 constexpr int kThreads = kWaves * 64;
-constexpr int kQB = kQueriesPerWave / 16;  // 16-row MFMA blocks per wavefront
 
 // ---------------------------------------------------------------------------
 // MFMA wrappers.  A operand: lane l holds row l%16, k-slice l/16.  B operand:
@@ -119,6 +116,28 @@ __device__ inline float to_f(T x) {
   return static_cast<float>(x);
 }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// s + a + b for two relative scores stored in T.  For 16-bit T the pair is
+// packed into one register and added with a single dot2 against (1, 1): the
+// products are exact and the sum is accumulated in fp32, so this equals the
+// two fp32 additions of the widened values up to fp32 rounding.
+template <typename T>
+__device__ inline float add_pair(float s, T a, T b) {
+  if constexpr (sizeof(T) == 4) {
+    return s + a + b;
+  } else if constexpr (__is_same(T, _Float16)) {
+    const half2_t v = {a, b};
+    const half2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    return __builtin_amdgcn_fdot2(v, one, s, false);
+  } else {
+    const bf16x2_t v = {a, b};
+    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(v, one, s, false);
+  }
+}
+
 // 16-byte global/LDS chunk copy.
 struct alignas(16) Chunk {
   uint32_t w[4];
@@ -146,15 +165,17 @@ constexpr int pad_of() {
 }
 constexpr int round16(int x) { return (x + 15) / 16 * 16; }
 
-template <typename T, int D, int BN>
+template <typename T, int D, int BN, int QW>
 struct Layout {
+  static constexpr int kQueriesPerWave = QW;                     // query rows per wavefront
+  static constexpr int kBlockM = kWaves * QW;                    // query rows per workgroup
   static constexpr int kPad = pad_of<T>();
   static constexpr int KS_LD = D + kPad;                         // Ks[BN][KS_LD]
-  static constexpr int VT_LD = BN + kPad;                        // Vt[D][VT_LD]
+  static constexpr int VT_LD = BN + 4;                           // Vt[D][VT_LD]
   static constexpr int WP_MAX = round16(kBlockM + BN - 1);       // p2c window
   static constexpr int PW_LD = WP_MAX + kPad;                    // Pw[BN][PW_LD]
   static constexpr int WC_MAX = round16(kQueriesPerWave + BN - 1);  // c2p window
-  static constexpr int CW_LD = WC_MAX + kPad;                    // Cw[w][32][CW_LD]
+  static constexpr int CW_LD = WC_MAX + kPad;                    // Cw[w][QW][CW_LD]
   static constexpr int LW_N = kBlockM + BN;                      // lut window
 
   static constexpr size_t ks_bytes = size_t(BN) * KS_LD * sizeof(T);
@@ -162,21 +183,28 @@ struct Layout {
   static constexpr size_t pw_bytes = size_t(BN) * PW_LD * sizeof(T);
   static constexpr size_t cw_bytes = size_t(kWaves) * kQueriesPerWave * CW_LD * sizeof(T);
   static constexpr size_t lw_bytes = size_t(LW_N) * sizeof(int32_t);
-  static constexpr size_t km_bytes = size_t(BN);
+  static constexpr size_t kb_bytes = size_t(BN) * sizeof(float);
 
+  // Offsets; Pw/Cw exist only for the windowed kernels.
   static constexpr size_t ks_off = 0;
   static constexpr size_t vt_off = ks_off + ks_bytes;
-  static constexpr size_t pw_off = vt_off + vt_bytes;
+  static constexpr size_t kb_off = vt_off + vt_bytes;
+  static constexpr size_t lw_off = kb_off + kb_bytes;
+  static constexpr size_t pw_off = lw_off + lw_bytes;
   static constexpr size_t cw_off = pw_off + pw_bytes;
-  static constexpr size_t lw_off = cw_off + cw_bytes;
-  static constexpr size_t km_off = lw_off + lw_bytes;
 
   static constexpr size_t bytes(bool windowed) {
-    size_t total = ks_bytes + vt_bytes + lw_bytes + km_bytes;
-    if (windowed) total += pw_bytes + cw_bytes;
-    return total;
+    return windowed ? cw_off + cw_bytes : pw_off;
   }
 };
+
+// Workgroup barrier that orders LDS traffic only.  __syncthreads() also waits
+// for every outstanding global load (vmcnt(0)), which would force the
+// next-tile prefetch to land at the first barrier; here global loads stay in
+// flight and are waited for where their registers are used.
+__device__ inline void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 __device__ inline int clampi(int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); }
 
@@ -192,30 +220,47 @@ __device__ inline int xcd_logical_block(int n, int total) {
   return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
 }
 
-template <typename T, int D, int BN, bool C2P, bool P2C, bool TABLE>
+// Four consecutive elements of T: one 8-byte (16-bit T) or 16-byte (fp32) access.
+template <typename T>
+using Quad = T __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ inline void store_quad(T* dst, f32x4_t acc) {
+  Quad<T> q;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) q[r] = to_t<T>(acc[r]);
+  *reinterpret_cast<Quad<T>*>(dst) = q;
+}
+
+template <typename T, int D, int BN, int QW, bool C2P, bool P2C, bool TABLE>
 __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
   using M = Mma<T>;
   using F = typename M::frag;
-  using LY = Layout<T, D, BN>;
-  constexpr bool WINDOWED = (C2P || P2C) && !TABLE;
+  using LY = Layout<T, D, BN, QW>;
+  constexpr int kBlockM = LY::kBlockM;
+  constexpr int kQB = QW / 16;         // 16-row MFMA blocks per wavefront
+  constexpr bool REL = C2P || P2C;
+  constexpr bool WINDOWED = REL && !TABLE;
   constexpr int KB = BN / 16;          // 16-key blocks per tile
   constexpr int DB = D / 16;           // 16-dim blocks of the output
   constexpr int KD = D / M::K;         // MFMA steps over the head dimension
   constexpr int E16 = 16 / sizeof(T);  // elements per 16-byte chunk
-  constexpr int CPR = D / E16;         // chunks per K/V row
+  constexpr int CPR = D / E16;         // 16-byte chunks per K row
   static_assert(BN % 32 == 0 || sizeof(T) == 4, "16-bit PV steps need 32-key groups");
 
   extern __shared__ __align__(16) unsigned char smem[];
   T* Ks = reinterpret_cast<T*>(smem + LY::ks_off);
   T* Vt = reinterpret_cast<T*>(smem + LY::vt_off);
+  float* Kbias = reinterpret_cast<float*>(smem + LY::kb_off);
+  int32_t* Lw = reinterpret_cast<int32_t*>(smem + LY::lw_off);
   T* Pw = reinterpret_cast<T*>(smem + LY::pw_off);
   T* Cw = reinterpret_cast<T*>(smem + LY::cw_off);
-  int32_t* Lw = reinterpret_cast<int32_t*>(smem + (WINDOWED ? LY::lw_off : LY::pw_off));
-  uint8_t* Km = smem + (WINDOWED ? LY::km_off : LY::pw_off + LY::lw_bytes);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wavefront index as a scalar: per-wave window bounds then use scalar loads.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
 
@@ -228,15 +273,17 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
   const int b = bh / H;
   const int h = bh - b * H;
   const int i0 = qblk * kBlockM;
-  const int i0w = i0 + wave * kQueriesPerWave;
+  const int i0w = i0 + wave * QW;
 
   const T* qg = reinterpret_cast<const T*>(p.q) + b * p.sb + h * p.sh;
   const T* kg = reinterpret_cast<const T*>(p.k) + b * p.sb + h * p.sh;
   const T* vg = reinterpret_cast<const T*>(p.v) + b * p.sb + h * p.sh;
   const uint8_t* maskb = p.mask + static_cast<int64_t>(b) * L;
+  const int sl = static_cast<int>(p.sl);  // row stride; L * sl < 2^31 is checked on the host
 
-  // Q fragments stay in registers for the whole kernel.  They serve as the B
-  // operand of K.Q^T and as the A operand of the c2p window product.
+  // Q fragments stay in registers for the whole kernel.  In the 16x16 MFMA
+  // layouts the A and B operands of a lane hold the same (row/column, k-slice),
+  // so these registers serve as B of K.Q^T and as B of Kr.Q^T.
   F qf[kQB][KD];
   bool qkept[kQB];
   bool qin[kQB];
@@ -270,99 +317,155 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
   const T* kr = posk + static_cast<int64_t>(h) * S * D;         // windowed only
   const T* qr = posq + static_cast<int64_t>(h) * S * D;         // windowed only
 
+  // ---- per-thread prefetch registers for the next tile ----
+  // K: 16-byte row chunks.  V: 4 keys x 4 dims blocks, transposed in registers
+  // and written to V^T as 4 packed stores.  Plus one LUT entry and one mask byte.
+  constexpr int NCH = (BN * CPR + kThreads - 1) / kThreads;
+  constexpr int VQD = D / 4;                                   // dim quads per row
+  constexpr int NVB = (BN / 4 * VQD + kThreads - 1) / kThreads;
+  constexpr int NLW = (kBlockM + BN - 1 + kThreads - 1) / kThreads;
+  constexpr bool K_EXACT = (BN * CPR) % kThreads == 0;
+  constexpr bool V_EXACT = (BN / 4 * VQD) % kThreads == 0;
+  u32x4_t pk[NCH];
+  Quad<T> pv[NVB][4];
+  int plut[NLW];
+  uint8_t pmask_raw = 0;  // mask byte of key jt + tid % BN (row clamped to L-1)
+  bool pmask_in = false;  // whether that key is inside the sequence
+  auto prefetch = [&](int jt) {
+#pragma unroll
+    for (int n = 0; n < NCH; ++n) {
+      const int t = tid + n * kThreads;
+      const int r = t / CPR;
+      const int cc = t - r * CPR;
+      // Rows past L are read from row L-1: finite values whose scores the key
+      // bias masks and whose probabilities are zero.
+      const int j = min(jt + r, L - 1);
+      if (K_EXACT || t < BN * CPR)
+        pk[n] = *reinterpret_cast<const u32x4_t*>(kg + (j * sl + cc * E16));
+    }
+#pragma unroll
+    for (int n = 0; n < NVB; ++n) {
+      const int t = tid + n * kThreads;
+      const int kq = t / VQD;
+      const int dq = t - kq * VQD;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int j = min(jt + 4 * kq + rr, L - 1);
+        if (V_EXACT || t < BN / 4 * VQD)
+          pv[n][rr] = *reinterpret_cast<const Quad<T>*>(vg + (j * sl + 4 * dq));
+      }
+    }
+    if constexpr (REL) {
+      const int dlo_t = i0 - (jt + BN - 1);
+#pragma unroll
+      for (int n = 0; n < NLW; ++n) {
+        const int t = tid + n * kThreads;
+        const int d = clampi(dlo_t + t, -(L - 1), L - 1);
+        plut[n] = p.lut[d + L - 1];
+      }
+    }
+    const int jm = jt + (tid % BN);
+    pmask_raw = maskb[min(jm, L - 1)];
+    pmask_in = jm < L;
+  };
+
+  // Window products run in batches of 16-slot chunks whose row fragments are
+  // fetched from global memory (L2-resident Kr/Qr) together.
+  constexpr int NSC_C = LY::WC_MAX / 16;                       // c2p chunks per wavefront
+  constexpr int CB = (12 / KD) < 1 ? 1 : ((12 / KD) > NSC_C ? NSC_C : (12 / KD));
+  constexpr int NSC_P = LY::WP_MAX / 16;                       // p2c chunks per workgroup
+  constexpr int PU = (NSC_P + kWaves - 1) / kWaves;            // p2c chunks per wavefront
+  constexpr int PB = (6 / KD) < 1 ? 1 : ((6 / KD) > PU ? PU : (6 / KD));
+
+  prefetch(0);
   for (int j0 = 0; j0 < L; j0 += BN) {
     // Delta window of this workgroup tile and of this wavefront.
     const int dlo = i0 - (j0 + BN - 1);
-    const int dlo_c = clampi(dlo, -(L - 1), L - 1);
-    const int dhi_c = clampi(i0 + kBlockM - 1 - j0, -(L - 1), L - 1);
+    const int dhi = i0 + kBlockM - 1 - j0;
     int lo_p = 0, w_p = 0, lo_c = 0, w_c = 0;
+    bool identity = false;
     if constexpr (WINDOWED) {
-      lo_p = p.lut[dlo_c + L - 1];
-      w_p = p.lut[dhi_c + L - 1] - lo_p + 1;
+      lo_p = p.lut[clampi(dlo, -(L - 1), L - 1) + L - 1];
+      w_p = p.lut[clampi(dhi, -(L - 1), L - 1) + L - 1] - lo_p + 1;
       const int dlo_w = clampi(i0w - (j0 + BN - 1), -(L - 1), L - 1);
-      const int dhi_w = clampi(i0w + kQueriesPerWave - 1 - j0, -(L - 1), L - 1);
+      const int dhi_w = clampi(i0w + QW - 1 - j0, -(L - 1), L - 1);
       lo_c = p.lut[dlo_w + L - 1];
       w_c = p.lut[dhi_w + L - 1] - lo_c + 1;
+      // Every delta of the tile has its own slot (inside the un-bucketed band,
+      // no clamping): the local slot is the window index itself.
+      identity = w_p == kBlockM + BN - 1 && dlo >= -(L - 1) && dhi <= L - 1;
       // A plan whose lookup table steps by more than one slot per delta breaks
       // the window precondition; clamp so LDS writes stay inside the buffers.
       w_p = min(w_p, LY::WP_MAX);
       w_c = min(w_c, LY::WC_MAX);
     }
+    const int nsc_p = (w_p + 15) >> 4;
+    const int nsc_c = (w_c + 15) >> 4;
 
-    __syncthreads();  // the previous tile is done with every LDS buffer
-
-    // ---- stage K (row-major), V^T, key mask and the delta -> slot window ----
-    for (int t = tid; t < BN * CPR; t += kThreads) {
-      const int r = t / CPR;
-      const int cc = t - r * CPR;
-      const int j = j0 + r;
-      Chunk kv{{0u, 0u, 0u, 0u}};
-      Chunk vv{{0u, 0u, 0u, 0u}};
-      if (j < L) {
-        kv = *reinterpret_cast<const Chunk*>(kg + static_cast<int64_t>(j) * p.sl + cc * E16);
-        vv = *reinterpret_cast<const Chunk*>(vg + static_cast<int64_t>(j) * p.sl + cc * E16);
-      }
-      *reinterpret_cast<Chunk*>(Ks + r * LY::KS_LD + cc * E16) = kv;
-      const T* ve = reinterpret_cast<const T*>(&vv);
+    // First batch of window row fragments, issued before the barrier so their
+    // latency overlaps the LDS staging below.
+    F bq[PB][KD];
+    F bk[CB][KD];
+    if constexpr (WINDOWED && P2C) {
 #pragma unroll
-      for (int e = 0; e < E16; ++e) Vt[(cc * E16 + e) * LY::VT_LD + r] = ve[e];
-    }
-    for (int t = tid; t < BN; t += kThreads) {
-      const int j = j0 + t;
-      Km[t] = (j < L) ? (maskb[j] != 0) : 0;
-    }
-    if constexpr (C2P || P2C) {
-      for (int t = tid; t < kBlockM + BN - 1; t += kThreads) {
-        const int d = clampi(dlo + t, -(L - 1), L - 1);
-        Lw[t] = p.lut[d + L - 1] - lo_p;
+      for (int u = 0; u < PB; ++u) {
+        const int sc = wave + kWaves * u;
+        const int s = min(lo_p + 16 * sc + c, S - 1);
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd)
+          bq[u][kd] = load_slice<T>(qr + (s * D + kd * M::K), g);
       }
     }
-    __syncthreads();
+    if constexpr (WINDOWED && C2P) {
+#pragma unroll
+      for (int u = 0; u < CB; ++u) {
+        const int s = min(lo_c + 16 * u + c, S - 1);
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd)
+          bk[u][kd] = load_slice<T>(kr + (s * D + kd * M::K), g);
+      }
+    }
 
-    // ---- relative-score windows (MFMA into LDS) ----
-    if constexpr (WINDOWED) {
-      if constexpr (P2C) {
-        // Pw[jr][s - lo_p] = K[j0 + jr] . Qr[s], shared by the workgroup.
-        const int nsc = (w_p + 15) >> 4;
-        for (int item = wave; item < KB * nsc; item += kWaves) {
-          const int kb = item / nsc;
-          const int sc = item - kb * nsc;
-          const int s = min(lo_p + 16 * sc + c, S - 1);
-          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+    lds_barrier();  // the previous tile is done with every LDS buffer
+
+    // ---- stage the prefetched tile: K, V^T, key bias, delta -> slot window ----
 #pragma unroll
-          for (int kd = 0; kd < KD; ++kd) {
-            F a = load_slice<T>(Ks + (16 * kb + c) * LY::KS_LD + kd * M::K, g);
-            F bq = load_slice<T>(qr + static_cast<int64_t>(s) * D + kd * M::K, g);
-            acc = M::run(a, bq, acc);
-          }
+    for (int n = 0; n < NCH; ++n) {
+      const int t = tid + n * kThreads;
+      if (K_EXACT || t < BN * CPR) {
+        const int r = t / CPR;
+        const int cc = t - r * CPR;
+        *reinterpret_cast<u32x4_t*>(Ks + r * LY::KS_LD + cc * E16) = pk[n];
+      }
+    }
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            Pw[(16 * kb + 4 * g + r) * LY::PW_LD + 16 * sc + c] = to_t<T>(acc[r]);
+    for (int n = 0; n < NVB; ++n) {
+      const int t = tid + n * kThreads;
+      if (V_EXACT || t < BN / 4 * VQD) {
+        const int kq = t / VQD;
+        const int dq = t - kq * VQD;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          Quad<T> col;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) col[rr] = pv[n][rr][e];
+          *reinterpret_cast<Quad<T>*>(Vt + (4 * dq + e) * LY::VT_LD + 4 * kq) = col;
         }
       }
-      if constexpr (C2P) {
-        // Cw[wave][q][s - lo_c] = Q[i0w + q] . Kr[s], private to the wavefront.
-        T* cw = Cw + wave * kQueriesPerWave * LY::CW_LD;
-        const int nsc = (w_c + 15) >> 4;
-        for (int sc = 0; sc < nsc; ++sc) {
-          const int s = min(lo_c + 16 * sc + c, S - 1);
-          F bk[KD];
-#pragma unroll
-          for (int kd = 0; kd < KD; ++kd)
-            bk[kd] = load_slice<T>(kr + static_cast<int64_t>(s) * D + kd * M::K, g);
-#pragma unroll
-          for (int qb = 0; qb < kQB; ++qb) {
-            f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kd = 0; kd < KD; ++kd) acc = M::run(qf[qb][kd], bk[kd], acc);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              cw[(16 * qb + 4 * g + r) * LY::CW_LD + 16 * sc + c] = to_t<T>(acc[r]);
-          }
-        }
-      }
-      __syncthreads();
     }
+    if (tid < BN) Kbias[tid] = (pmask_in && pmask_raw != 0) ? 0.0f : -INFINITY;
+    if constexpr (REL) {
+#pragma unroll
+      for (int n = 0; n < NLW; ++n) {
+        const int t = tid + n * kThreads;
+        if (t < kBlockM + BN - 1) Lw[t] = plut[n] - lo_p;
+      }
+    }
+    lds_barrier();
+
+    auto kfrag = [&](int kb, int kd) -> F {
+      return load_slice<T>(Ks + (16 * kb + c) * LY::KS_LD + kd * M::K, g);
+    };
 
     // ---- S^T = K . Q^T ----
     f32x4_t sc_acc[KB][kQB];
@@ -374,60 +477,191 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
     for (int kd = 0; kd < KD; ++kd) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        F a = load_slice<T>(Ks + (16 * kb + c) * LY::KS_LD + kd * M::K, g);
+        const F a = kfrag(kb, kd);
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) sc_acc[kb][qb] = M::run(a, qf[qb][kd], sc_acc[kb][qb]);
       }
     }
 
-    // ---- relative scores, scale, mask, online softmax ----
-    const T* cw = Cw + wave * kQueriesPerWave * LY::CW_LD;
-    const int c_shift = lo_c - lo_p;
+    // ---- relative-score windows: transposed products, 4 packed slots per lane ----
+    if constexpr (WINDOWED) {
+      if constexpr (P2C) {
+        // Pw[jr][s - lo_p] = Qr[s] . K[j0 + jr]; chunk sc belongs to wavefront sc % 4.
+        for (int base = 0; base < PU; base += PB) {
+          if (wave + kWaves * base >= nsc_p) break;
+          if (base > 0) {
 #pragma unroll
-    for (int qb = 0; qb < kQB; ++qb) {
-      const int iq = 16 * qb + c;        // query row inside the wavefront
-      const int i = i0w + iq;
-      float tile_max = -INFINITY;
+            for (int u = 0; u < PB; ++u) {
+              const int sc = wave + kWaves * (base + u);
+              const int s = min(lo_p + 16 * sc + c, S - 1);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int jr = 16 * kb + 4 * g + r;
-          const int j = j0 + jr;
-          float s = sc_acc[kb][qb][r];
-          if constexpr (C2P || P2C) {
-            const int ls = Lw[i - j - dlo];
-            if constexpr (TABLE) {
-              const bool ok = qin[qb] && j < L;
-              if constexpr (C2P)
-                if (ok) s += to_f<T>(c2p_rows[static_cast<int64_t>(i) * S + ls]);
-              if constexpr (P2C)
-                if (ok) s += to_f<T>(p2c_rows[static_cast<int64_t>(j) * S + ls]);
-            } else {
-              if constexpr (C2P) s += to_f<T>(cw[iq * LY::CW_LD + ls - c_shift]);
-              if constexpr (P2C) s += to_f<T>(Pw[jr * LY::PW_LD + ls]);
+              for (int kd = 0; kd < KD; ++kd)
+                bq[u][kd] = load_slice<T>(qr + (s * D + kd * M::K), g);
             }
           }
-          float x = s * p.scale_log2;
-          const bool kin = j < L;
-          const bool kkept = Km[jr] != 0;
-          if (!(qkept[qb] && kkept)) {
-            if (qin[qb]) {
-              x = (!qkept[qb] && kin) ? 0.0f : -INFINITY;
-            } else {
-              x = (j == 0) ? 0.0f : -INFINITY;
+#pragma unroll
+          for (int u = 0; u < PB; ++u) {
+            const int sc = wave + kWaves * (base + u);
+            if (sc >= nsc_p) break;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+              f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int kd = 0; kd < KD; ++kd) acc = M::run(bq[u][kd], kfrag(kb, kd), acc);
+              store_quad<T>(Pw + (16 * kb + c) * LY::PW_LD + 16 * sc + 4 * g, acc);
             }
           }
-          sc_acc[kb][qb][r] = x;
-          tile_max = fmaxf(tile_max, x);
         }
       }
-      tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16));
-      tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-      const float new_max = fmaxf(row_max[qb], tile_max);
-      const float base = new_max == -INFINITY ? 0.0f : new_max;
-      const float corr = __builtin_amdgcn_exp2f(row_max[qb] - base);
-      row_max[qb] = new_max;
+      if constexpr (C2P) {
+        // Cw[wave][q][s - lo_c] = Kr[s] . Q[i0w + q], private to the wavefront.
+        T* cwp = Cw + wave * QW * LY::CW_LD;
+        for (int base = 0; base < nsc_c; base += CB) {
+          if (base > 0) {
+#pragma unroll
+            for (int u = 0; u < CB; ++u) {
+              const int s = min(lo_c + 16 * (base + u) + c, S - 1);
+#pragma unroll
+              for (int kd = 0; kd < KD; ++kd)
+                bk[u][kd] = load_slice<T>(kr + (s * D + kd * M::K), g);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < CB; ++u) {
+            if (base + u >= nsc_c) break;
+#pragma unroll
+            for (int qb = 0; qb < kQB; ++qb) {
+              f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int kd = 0; kd < KD; ++kd) acc = M::run(bk[u][kd], qf[qb][kd], acc);
+              store_quad<T>(cwp + (16 * qb + c) * LY::CW_LD + 16 * (base + u) + 4 * g, acc);
+            }
+          }
+        }
+      }
+    }
+    // Next tile's K/V/LUT/mask: issued after every load this tile consumes
+    // (vector-memory counters retire in order), in flight during the softmax.
+    // Unconditional (the last tile re-reads clamped rows) so that no branch
+    // joins pending loads, which would force early waits on them.
+    prefetch(j0 + BN);
+    if constexpr (WINDOWED) lds_barrier();
+
+    // ---- relative scores, scale, key bias ----
+    // LDS addresses are a per-lane base plus compile-time offsets:
+    //   window index of (i, j): i - j - dlo = lane_base + 16*(qb - kb) - r
+    //   with lane_base = wave*QW + c - 4g + BN - 1; Pw row of key j: 16kb + 4g + r.
+    const int lane_base = wave * QW + c - 4 * g + BN - 1;
+    const int32_t* lw_lane = Lw + lane_base;
+    const T* cw_lane = Cw + (wave * QW + c) * LY::CW_LD - (lo_c - lo_p);
+    const T* pw_lane = Pw + 4 * g * LY::PW_LD;
+    f32x4_t kbias[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+      kbias[kb] = *reinterpret_cast<const f32x4_t*>(Kbias + 16 * kb + 4 * g);
+    const float scale = p.scale_log2;
+
+    auto relative = [&](int qb, int kb, int r, int ls) -> float {
+      float add = 0.0f;
+      if constexpr (TABLE) {
+        const int i = i0w + 16 * qb + c;
+        const int j = j0 + 16 * kb + 4 * g + r;
+        const bool ok = qin[qb] && j < L;
+        if constexpr (C2P)
+          if (ok) add += to_f<T>(c2p_rows[static_cast<int64_t>(i) * S + ls]);
+        if constexpr (P2C)
+          if (ok) add += to_f<T>(p2c_rows[static_cast<int64_t>(j) * S + ls]);
+      }
+      return add;
+    };
+    if constexpr (WINDOWED) {
+      if (identity) {
+        // Local slot = window index: pure immediate-offset gathers.
+        const T* cw_id = cw_lane + lane_base;
+        const T* pw_id = pw_lane + lane_base;
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int off = 16 * (qb - kb) - r;
+              const T cv = C2P ? cw_id[16 * qb * LY::CW_LD + off] : static_cast<T>(0.0f);
+              const T pv2 = P2C ? pw_id[(16 * kb + r) * LY::PW_LD + off] : static_cast<T>(0.0f);
+              const float s = add_pair<T>(sc_acc[kb][qb][r], cv, pv2);
+              sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
+            }
+      } else {
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int ls = lw_lane[16 * (qb - kb) - r];
+              const T cv = C2P ? cw_lane[16 * qb * LY::CW_LD + ls] : static_cast<T>(0.0f);
+              const T pv2 = P2C ? pw_lane[(16 * kb + r) * LY::PW_LD + ls] : static_cast<T>(0.0f);
+              const float s = add_pair<T>(sc_acc[kb][qb][r], cv, pv2);
+              sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
+            }
+      }
+    } else {
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float s = sc_acc[kb][qb][r];
+            if constexpr (REL) s += relative(qb, kb, r, lw_lane[16 * (qb - kb) - r]);
+            sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
+          }
+    }
+
+    // ---- padded and out-of-range query rows (rare; wavefront-uniform branch) ----
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      if (__any(!qkept[qb])) {
+        if (!qkept[qb]) {
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int j = j0 + 16 * kb + 4 * g + r;
+              // padded row: uniform over in-range keys; row past L: key 0 only
+              const bool hit = qin[qb] ? (j < L) : (j == 0);
+              sc_acc[kb][qb][r] = hit ? 0.0f : -INFINITY;
+            }
+        }
+      }
+    }
+
+    // ---- online softmax ----
+    // The exponent base of a row only has to be common to the row and keep
+    // exp2 finite, so the previous maximum is reused while no score exceeds it
+    // by more than kSlack (p <= 2^kSlack); only then are the row maxima reduced
+    // across lanes and the accumulators rescaled.  Wavefront-uniform branch.
+    constexpr float kSlack = 8.0f;
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      float lane_max = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lane_max = fmaxf(lane_max, sc_acc[kb][qb][r]);
+      if (__any(lane_max > row_max[qb] + kSlack)) {
+        float tile_max = fmaxf(lane_max, __shfl_xor(lane_max, 16));
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        const float new_max = fmaxf(row_max[qb], tile_max);
+        const float old_base = row_max[qb] == -INFINITY ? 0.0f : row_max[qb];
+        const float new_base = new_max == -INFINITY ? 0.0f : new_max;
+        const float corr = __builtin_amdgcn_exp2f(old_base - new_base);
+        row_max[qb] = new_max;
+        row_sum[qb] *= corr;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db][qb] *= corr;
+      }
+      const float base = row_max[qb] == -INFINITY ? 0.0f : row_max[qb];
       float psum = 0.0f;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
@@ -437,9 +671,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
           sc_acc[kb][qb][r] = pr;
           psum += pr;
         }
-      row_sum[qb] = row_sum[qb] * corr + psum;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) o[db][qb] *= corr;
+      row_sum[qb] += psum;
     }
 
     // ---- O^T += V^T . P^T ----
@@ -458,11 +690,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const T* vrow = Vt + (16 * db + c) * LY::VT_LD + 32 * ks + 4 * g;
+          const Quad<T> lo = *reinterpret_cast<const Quad<T>*>(vrow);
+          const Quad<T> hi = *reinterpret_cast<const Quad<T>*>(vrow + 16);
           F a;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            a[r] = vrow[r];
-            a[4 + r] = vrow[16 + r];
+            a[r] = lo[r];
+            a[4 + r] = hi[r];
           }
 #pragma unroll
           for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
@@ -517,18 +751,28 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
 // ---------------------------------------------------------------------------
 // Host-side dispatch
 // ---------------------------------------------------------------------------
+// Tile configuration per (dtype, head dim): keys per tile and query rows per
+// wavefront.  d=128 halves the rows per wavefront to stay within 256 VGPRs at
+// two wavefronts per SIMD.
 template <typename T, int D>
 constexpr int block_n() {
   return sizeof(T) == 4 ? 32 : 64;
 }
+template <typename T, int D>
+constexpr int queries_per_wave() {
+  return D >= 128 ? 16 : 32;
+}
 
 template <typename T, int D, bool C2P, bool P2C, bool TABLE>
-int launch(const Params& prm, hipStream_t stream) {
+int launch(const Params& base, hipStream_t stream) {
   constexpr int BN = block_n<T, D>();
-  using LY = Layout<T, D, BN>;
+  constexpr int QW = queries_per_wave<T, D>();
+  using LY = Layout<T, D, BN, QW>;
   constexpr bool WINDOWED = (C2P || P2C) && !TABLE;
+  Params prm = base;
+  prm.nqb = (prm.L + LY::kBlockM - 1) / LY::kBlockM;
   const size_t lds = LY::bytes(WINDOWED);
-  auto kernel = attention_kernel<T, D, BN, C2P, P2C, TABLE>;
+  auto kernel = attention_kernel<T, D, BN, QW, C2P, P2C, TABLE>;
   hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(lds));
@@ -572,6 +816,9 @@ int check_common(const void* q, const void* k, const void* v, const int32_t* lut
   if (B < 1 || H < 1 || L < 1) return DFLASH_ERR_SHAPE;
   if (D != 32 && D != 64 && D != 128) return DFLASH_ERR_HEAD_DIM;
   if (dtype < DFLASH_DTYPE_FP16 || dtype > DFLASH_DTYPE_FP32) return DFLASH_ERR_DTYPE;
+  if (static_cast<int64_t>(L) * D >= (int64_t{1} << 31) ||
+      static_cast<int64_t>(S) * D >= (int64_t{1} << 31))
+    return DFLASH_ERR_TOO_LARGE;
   if (has_c2p || has_p2c) {
     if (!lut) return DFLASH_ERR_NULL;
     if (S < 1) return DFLASH_ERR_SHAPE;
@@ -611,7 +858,6 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
   prm.H = H;
   prm.L = L;
   prm.S = (has_c2p || has_p2c) ? S : 1;
-  prm.nqb = (L + kBlockM - 1) / kBlockM;
   prm.scale_log2 = score_scale_log2;
   return dispatch<true>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
 }
@@ -630,6 +876,7 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
   if ((has_c2p && !pos_key) || (has_p2c && !pos_query)) return DFLASH_ERR_NULL;
   const int esize = dtype == DFLASH_DTYPE_FP32 ? 4 : 2;
   if (stride_l < D || stride_b < 1 || stride_h < 1) return DFLASH_ERR_SHAPE;
+  if (static_cast<int64_t>(L) * stride_l >= (int64_t{1} << 31)) return DFLASH_ERR_TOO_LARGE;
   if (((stride_b | stride_h | stride_l) * esize) % 16 != 0) return DFLASH_ERR_ALIGN;
   const uintptr_t addr_or = reinterpret_cast<uintptr_t>(query) |
                             reinterpret_cast<uintptr_t>(key) |
@@ -654,7 +901,6 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
   prm.H = H;
   prm.L = L;
   prm.S = (has_c2p || has_p2c) ? S : 1;
-  prm.nqb = (L + kBlockM - 1) / kBlockM;
   prm.scale_log2 = score_scale_log2;
   return dispatch<false>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
 }

@@ -34,6 +34,16 @@ def optimized_attention(hidden: torch.Tensor, qkv_weight: torch.Tensor,
         return t.view(batch, length, num_heads, head_dim).permute(0, 2, 1, 3).contiguous()
 
     q, k, v = (heads(t) for t in fused.split(width, dim=-1))
+    return optimized_core(q, k, v, pos_key, pos_query, pair_to_local, mask, scale)
+
+
+def optimized_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   pos_key: torch.Tensor | None, pos_query: torch.Tensor | None,
+                   pair_to_local: torch.Tensor, mask: torch.Tensor, scale: float) -> torch.Tensor:
+    """Attention part of ``_torch.py:339-387`` from head-major ``q/k/v [B, H, L, d]``."""
+
+    batch, num_heads, length, head_dim = q.shape
+    width = num_heads * head_dim
     scores = torch.matmul(q, k.transpose(-1, -2) / scale)
     index = pair_to_local.expand(batch, num_heads, length, length)
     if pos_key is not None:

@@ -1,0 +1,242 @@
+"""Module- and encoder-level parity of the HIP backend with the Hugging Face original.
+
+The reference's ``original`` backend is a verbatim copy of transformers'
+``DisentangledSelfAttention``; the installed transformers provides the same
+equation on the GPU box, so it is the comparator here (same seeded weights and
+inputs).  Attention-output tolerances (max-abs): fp16 2e-3, bf16 1e-2, fp32 1e-5.
+"""
+
+from __future__ import annotations
+
+import copy
+import types
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5}
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+MODES = {"both": ("c2p", "p2c"), "c2p": ("c2p",), "p2c": ("p2c",)}
+
+
+def _hf_attention(hidden, heads, head_dim, modes, share=True, buckets=256, max_rel=512):
+    from transformers.models.deberta_v2.modeling_deberta_v2 import DisentangledSelfAttention
+
+    cfg = types.SimpleNamespace(
+        hidden_size=hidden, num_attention_heads=heads, attention_head_size=head_dim,
+        share_att_key=share, pos_att_type=list(modes), relative_attention=True,
+        position_buckets=buckets, max_relative_positions=max_rel, max_position_embeddings=512,
+        hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0,
+    )
+    return DisentangledSelfAttention(cfg), cfg
+
+
+def _init(module, seed):
+    gen = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, param in module.named_parameters():
+            if name.endswith("weight"):
+                param.copy_(torch.randn(param.shape, generator=gen) * 0.02)
+            else:
+                param.zero_()
+
+
+def _hip_from_hf(hf_module, cfg, dtype, mode="fused"):
+    from disentangled_flash.kernel import HipInferenceDisentangledSelfAttention
+    from disentangled_flash.modeling import DebertaAttentionConfig
+
+    config = DebertaAttentionConfig(
+        hidden_size=cfg.hidden_size, num_attention_heads=cfg.num_attention_heads,
+        attention_head_size=cfg.attention_head_size, relative_attention=True,
+        position_buckets=cfg.position_buckets, max_relative_positions=cfg.max_relative_positions,
+        pos_att_type=tuple(cfg.pos_att_type), share_att_key=cfg.share_att_key,
+        hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0,
+    )
+    module = HipInferenceDisentangledSelfAttention(config, relative_mode=mode)
+    module.load_state_dict(hf_module.state_dict(), strict=True)
+    return module.to("cuda", dtype).eval()
+
+
+def _inputs(batch, length, hidden, lengths, seed, span):
+    gen = torch.Generator().manual_seed(seed)
+    states = torch.randn(batch, length, hidden, generator=gen)
+    rel = torch.randn(2 * span, hidden, generator=gen) * 0.02
+    mask = torch.arange(length)[None] < torch.as_tensor(lengths)[:, None]
+    return states, rel, mask
+
+
+def _run_pair(hf_module, hip_module, states, rel, mask, dtype):
+    """(hip output in dtype, HF output in dtype, HF output in float64)."""
+
+    m = mask.cuda()
+    pair = m[:, None, None, :] & m[:, None, :, None]
+    outs = []
+    with torch.inference_mode():
+        for precision in (dtype, torch.float64):
+            ref = copy.deepcopy(hf_module).to("cuda", precision).eval()
+            outs.append(ref(states.to("cuda", precision), pair,
+                            rel_embeddings=rel.to("cuda", precision))[0])
+        hip_module.prepare_for_inference(rel.to("cuda", dtype))
+        got, _ = hip_module(states.to("cuda", dtype), m)
+        torch.cuda.synchronize()
+    return got, outs[0], outs[1]
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("mode", ["fused", "table"])
+def test_c1_layer_matches_huggingface(dtype, mode):
+    """BASELINE config 1 shape: v3-base layer, B=2, L=128, lengths U[64, 128]."""
+
+    torch_dtype = DTYPES[dtype]
+    hf_module, cfg = _hf_attention(768, 12, 64, ("c2p", "p2c"))
+    _init(hf_module, 17)
+    gen = torch.Generator().manual_seed(18)
+    lengths = torch.randint(64, 129, (2,), generator=gen)
+    states, rel, mask = _inputs(2, 128, 768, lengths, 19, 256)
+    hip = _hip_from_hf(hf_module, cfg, torch_dtype, mode)
+    got, same_dtype, exact = _run_pair(hf_module, hip, states, rel, mask, torch_dtype)
+    err = (got.double() - same_dtype.double()).abs().max().item()
+    err64 = (got.double() - exact).abs().max().item()
+    ref_err = (same_dtype.double() - exact).abs().max().item()
+    print(f"C1 {dtype} {mode}: vs HF same dtype {err:.2e}, vs fp64 {err64:.2e} (HF {ref_err:.2e})")
+    assert err <= TOL[torch_dtype]
+    assert err64 <= TOL[torch_dtype]
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("mode", list(MODES))
+@pytest.mark.parametrize("shape", ["d128", "d32"])
+def test_c5_edge_sweep(dtype, mode, shape):
+    """d=128/H=8 at B=16 L=512 and d=32/H=16 at B=16 L=384."""
+
+    heads, head_dim, length = (8, 128, 512) if shape == "d128" else (16, 32, 384)
+    torch_dtype = DTYPES[dtype]
+    hidden = heads * head_dim
+    hf_module, cfg = _hf_attention(hidden, heads, head_dim, MODES[mode])
+    _init(hf_module, 31)
+    boundary = torch.tensor([1, 63, 64, 65, 127, 129, 383, 384, 511, 512]).clamp(max=length)
+    lengths = boundary[torch.arange(16) % 10]
+    states, rel, mask = _inputs(16, length, hidden, lengths, 32, 256)
+    hip = _hip_from_hf(hf_module, cfg, torch_dtype)
+    got, same_dtype, exact = _run_pair(hf_module, hip, states, rel, mask, torch_dtype)
+    err = (got.double() - same_dtype.double()).abs().max().item()
+    err64 = (got.double() - exact).abs().max().item()
+    print(f"C5 {shape} {dtype} {mode}: vs HF {err:.2e}, vs fp64 {err64:.2e}")
+    assert err <= TOL[torch_dtype]
+    assert err64 <= TOL[torch_dtype]
+
+
+def _encoder_model(layers, hidden, heads, ffn, buckets=256):
+    from transformers import DebertaV2Config, DebertaV2Model
+
+    config = DebertaV2Config(
+        vocab_size=128100, hidden_size=hidden, num_hidden_layers=layers,
+        num_attention_heads=heads, intermediate_size=ffn, hidden_act="gelu",
+        hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0, max_position_embeddings=512,
+        type_vocab_size=0, initializer_range=0.02, layer_norm_eps=1e-7, relative_attention=True,
+        max_relative_positions=-1, position_buckets=buckets, pos_att_type=["p2c", "c2p"],
+        norm_rel_ebd="layer_norm", share_att_key=True, conv_kernel_size=3, conv_act="gelu",
+        position_biased_input=False,
+    )
+    torch.manual_seed(17)
+    return DebertaV2Model(config).eval()
+
+
+def _encoder_inputs(batch, length, hidden, seed=19):
+    gen = torch.Generator().manual_seed(seed)
+    table = torch.randn(4096, hidden, generator=gen) * 0.02
+    table[0].zero_()
+    tokens = torch.randint(1, 4096, (batch, length), generator=gen)
+    lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen)
+    mask = torch.arange(length)[None] < lengths[:, None]
+    tokens = tokens.masked_fill(~mask, 0)
+    return table[tokens], mask.long()
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_12_layer_encoder_matches_huggingface(dtype):
+    """BASELINE config 3 architecture at B=8, L=256: final hidden states vs HF.
+
+    The HIP encoder in ``dtype`` must stay as close to the float32 HF encoder as
+    HF's own encoder in ``dtype`` does (within 1.5x + the attention tolerance);
+    in fp32 both are held to 1e-4 on LayerNorm-scale outputs.
+    """
+
+    from disentangled_flash import enable_deberta_inference
+
+    torch_dtype = DTYPES[dtype]
+    base = _encoder_model(12, 768, 12, 3072)
+    hidden, mask = _encoder_inputs(8, 256, 768)
+    hidden, mask = hidden.cuda(), mask.cuda()
+    with torch.inference_mode():
+        ref32 = copy.deepcopy(base).to("cuda", torch.float32).encoder
+        exact = ref32(hidden.float(), mask, output_hidden_states=False).last_hidden_state
+        ref = copy.deepcopy(base).to("cuda", torch_dtype).encoder
+        same = ref(hidden.to(torch_dtype), mask, output_hidden_states=False).last_hidden_state
+        fast = enable_deberta_inference(copy.deepcopy(base).to("cuda", torch_dtype),
+                                        backend="hip", sequence_lengths=[256])
+        got = fast.encoder(hidden.to(torch_dtype), mask,
+                           output_hidden_states=False).last_hidden_state
+    valid = mask.bool()[..., None]
+    err = ((got.float() - exact).abs() * valid).max().item()
+    ref_err = ((same.float() - exact).abs() * valid).max().item()
+    err_same = ((got.float() - same.float()).abs() * valid).max().item()
+    print(f"encoder {dtype}: hip-vs-fp32 {err:.2e}, HF-{dtype}-vs-fp32 {ref_err:.2e}, "
+          f"hip-vs-HF-{dtype} {err_same:.2e}")
+    if torch_dtype == torch.float32:
+        assert err <= 1e-4
+    else:
+        assert err <= 1.5 * ref_err + TOL[torch_dtype]
+
+
+def test_xlarge_bf16_buckets():
+    """BASELINE config 4 (shortened to 4 layers): hidden 1536, 24 heads, bf16, buckets."""
+
+    from disentangled_flash import enable_deberta_inference
+
+    base = _encoder_model(4, 1536, 24, 6144)
+    fast = enable_deberta_inference(copy.deepcopy(base).to("cuda", torch.bfloat16),
+                                    backend="hip", sequence_lengths=[64, 128, 256])
+    ref32 = copy.deepcopy(base).to("cuda", torch.float32).encoder
+    ref16 = copy.deepcopy(base).to("cuda", torch.bfloat16).encoder
+    gen = torch.Generator().manual_seed(5)
+    for bucket in (64, 128, 256):
+        hidden, mask = _encoder_inputs(8, bucket, 1536, seed=bucket)
+        lengths = torch.exp(torch.randn(8, generator=gen) * 0.5 + 4.09).clamp(16, bucket).long()
+        mask = (torch.arange(bucket)[None] < lengths[:, None]).long()
+        hidden, mask = hidden.cuda(), mask.cuda()
+        with torch.inference_mode():
+            fast.encoder.activate_shape(bucket)
+            got = fast.encoder(hidden.bfloat16(), mask, output_hidden_states=False)[0]
+            exact = ref32(hidden.float(), mask, output_hidden_states=False)[0]
+            same = ref16(hidden.bfloat16(), mask, output_hidden_states=False)[0]
+        valid = mask.bool()[..., None]
+        err = ((got.float() - exact).abs() * valid).max().item()
+        ref_err = ((same.float() - exact).abs() * valid).max().item()
+        print(f"xlarge bf16 L={bucket}: hip {err:.2e}, HF bf16 {ref_err:.2e}")
+        assert err <= 1.5 * ref_err + TOL[torch.bfloat16]
+
+
+def test_optimize_deberta_on_full_model_and_compile():
+    """Public API end to end, including torch.compile(fullgraph=True) of a bucket."""
+
+    from disentangled_flash import compile_deberta_buckets, optimize_deberta
+
+    base = _encoder_model(2, 256, 4, 512, buckets=64).to("cuda", torch.float16)
+    model = optimize_deberta(copy.deepcopy(base), sequence_lengths=[64])
+    ids = torch.randint(1, 1000, (4, 64), device="cuda")
+    mask = (torch.arange(64, device="cuda")[None] < torch.tensor([[64], [40], [9], [1]],
+                                                                 device="cuda")).long()
+    with torch.inference_mode():
+        expected = base(input_ids=ids, attention_mask=mask).last_hidden_state
+        got = model(input_ids=ids, attention_mask=mask).last_hidden_state
+        hidden = model.embeddings(input_ids=ids, mask=mask)
+        compiled = compile_deberta_buckets(model.encoder, [64], mode="default")
+        traced = compiled[64](hidden, mask)
+        eager = model.encoder(hidden, mask, output_hidden_states=False).last_hidden_state
+    valid = mask.bool()[..., None]
+    assert ((got.float() - expected.float()).abs() * valid).max().item() <= 2e-2
+    # Inductor re-fuses the fp16 LayerNorm/GELU epilogues; outputs are O(1) in fp16.
+    assert (traced.float() - eager.float()).abs().max().item() <= 1e-2

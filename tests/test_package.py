@@ -1,0 +1,263 @@
+"""CPU tests of the package: public API, plans, torch backend, encoder wrapper, C ABI exports."""
+
+from __future__ import annotations
+
+import copy
+import math
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import REPO, load_case
+from oracle.attention import original_attention
+from oracle.positions import compact_plan
+
+
+def test_public_api_imports():
+    import disentangled_flash as df
+
+    assert callable(df.optimize_deberta)
+    assert callable(df.enable_deberta_inference)
+    assert callable(df.compile_deberta_buckets)
+    assert df.DisentangledFlashAttention.__name__ == "HipInferenceDisentangledSelfAttention"
+    assert re.match(r"^\d+\.\d+\.\d+$", df.__version__)
+
+
+def test_position_plan_matches_oracle():
+    from disentangled_flash.position import SharedPositionPlanCache
+
+    cache = SharedPositionPlanCache(position_buckets=256, max_relative_positions=512,
+                                    position_embedding_size=256)
+    for length in (1, 17, 65, 128, 129, 384, 512, 700):
+        plan = cache.compact(length, "cpu")
+        active, lut = compact_plan(length, position_buckets=256, max_relative_positions=512,
+                                   position_embedding_size=256)
+        np.testing.assert_array_equal(plan.active_slots.numpy(), active)
+        np.testing.assert_array_equal(plan.delta_to_local.numpy(), lut)
+        assert plan.delta_to_local.dtype == torch.int32
+    assert cache.compact(65, "cpu") is cache.compact(65, "cpu")
+    dense = cache.dense(9, "cpu")
+    assert dense.pair_to_local.shape == (1, 1, 9, 9)
+    with pytest.raises(ValueError):
+        cache.compact(0, "cpu")
+
+
+def test_window_precondition_holds_for_standard_plans():
+    from disentangled_flash.kernel import lut_is_window_safe
+
+    for buckets, maximum in ((256, 512), (16, 64), (-1, 16), (8, 32)):
+        span = buckets if buckets > 0 else maximum
+        _, lut = compact_plan(600, position_buckets=buckets, max_relative_positions=maximum,
+                              position_embedding_size=span)
+        assert lut_is_window_safe(torch.from_numpy(lut))
+    assert not lut_is_window_safe(torch.tensor([0, 2, 3], dtype=torch.int32))
+
+
+def _config(case_spec, **overrides):
+    from disentangled_flash.modeling import DebertaAttentionConfig
+
+    fields = dict(
+        hidden_size=case_spec.hidden_size, num_attention_heads=case_spec.num_heads,
+        attention_head_size=case_spec.head_dim, relative_attention=True,
+        max_relative_positions=case_spec.max_relative_positions,
+        position_buckets=case_spec.position_buckets, share_att_key=case_spec.share_att_key,
+        pos_att_type=case_spec.pos_att_type, hidden_dropout_prob=0.0,
+        attention_probs_dropout_prob=0.0, norm_rel_ebd="none",
+    )
+    fields.update(overrides)
+    return DebertaAttentionConfig(**fields)
+
+
+def _load_params(module, params):
+    with torch.no_grad():
+        for name, value in params.items():
+            proj, kind = name.rsplit("_", 1)
+            getattr(module, f"{proj}_proj").__getattr__(kind).copy_(torch.from_numpy(value))
+
+
+@pytest.mark.parametrize("case", ["v3_small", "c2p_separate_buckets16", "p2c_d128_unbucketed",
+                                  "fully_masked_row", "length1"])
+def test_original_module_matches_golden(case):
+    from disentangled_flash.modeling import DisentangledSelfAttention
+
+    spec, params, hidden, rel, mask, expected = load_case(case)
+    module = DisentangledSelfAttention(_config(spec)).double().eval()
+    _load_params(module, params)
+    m = torch.from_numpy(mask)
+    pair = m[:, None, None, :] & m[:, None, :, None]
+    with torch.no_grad():
+        out, _ = module(torch.from_numpy(hidden).double(), pair,
+                        rel_embeddings=torch.from_numpy(rel).double())
+    np.testing.assert_allclose(out.numpy(), expected, atol=1e-10)
+
+
+@pytest.mark.parametrize("case", ["v3_small", "c2p_separate_buckets16", "p2c_d128_unbucketed",
+                                  "fully_masked_row", "no_relative"])
+def test_torch_backend_matches_oracle(case):
+    from disentangled_flash._torch import TorchInferenceDisentangledSelfAttention
+
+    spec, params, hidden, rel, mask, _ = load_case(case)
+    module = TorchInferenceDisentangledSelfAttention(_config(spec)).double().eval()
+    _load_params(module, params)
+    module.prepare_for_inference(torch.from_numpy(rel).double())
+    with torch.inference_mode():
+        out, _ = module(torch.from_numpy(hidden).double(), torch.from_numpy(mask))
+    exact = original_attention(spec, params, hidden, rel, mask,
+                               scale=math.sqrt(spec.head_dim * spec.scale_factor))
+    np.testing.assert_allclose(out.numpy(), exact, atol=1e-10)
+
+
+def test_qkv_is_always_fused_after_prepare():
+    """Reference tests/test_fused_qkv.py:7-30."""
+
+    from disentangled_flash._torch import TorchInferenceDisentangledSelfAttention
+    from disentangled_flash.modeling import DebertaAttentionConfig
+
+    config = DebertaAttentionConfig(
+        hidden_size=64, num_attention_heads=1, attention_head_size=64, relative_attention=True,
+        max_relative_positions=64, max_position_embeddings=64, position_buckets=32,
+        share_att_key=True, pos_att_type=("c2p", "p2c"), norm_rel_ebd="none",
+    )
+    module = TorchInferenceDisentangledSelfAttention(config).eval()
+    module.prepare_for_inference(torch.randn(config.position_buckets * 2, config.hidden_size))
+    assert module._cached_qkv_weight.shape == (192, 64)
+    with torch.inference_mode():
+        q, k, v = module._project_qkv(torch.randn(2, 8, 64))
+    assert q.shape == k.shape == v.shape == (2, 8, 64)
+
+
+def test_inference_guards_and_cache_invalidation():
+    from disentangled_flash._torch import TorchInferenceDisentangledSelfAttention
+    from disentangled_flash.modeling import DebertaAttentionConfig
+
+    module = TorchInferenceDisentangledSelfAttention(DebertaAttentionConfig(hidden_size=64,
+                                                                            num_attention_heads=2))
+    with pytest.raises(RuntimeError, match="eval"):
+        module.prepare_for_inference(torch.randn(512, 64))
+    module.eval().prepare_for_inference(torch.randn(512, 64))
+    with pytest.raises(RuntimeError, match="no_grad"):
+        module(torch.randn(1, 4, 64), torch.ones(1, 4))
+    assert module._cached_qkv_weight is not None
+    module.load_state_dict(module.state_dict())
+    assert module._cached_qkv_weight is None
+    module.prepare_for_inference(torch.randn(512, 64))
+    module.double()
+    assert module._cached_qkv_weight is None
+    module.prepare_for_inference(torch.randn(512, 64, dtype=torch.float64))
+    module.train()
+    assert module._cached_qkv_weight is None
+
+
+def test_hip_module_validation_errors_on_cpu():
+    from disentangled_flash.kernel import HipInferenceDisentangledSelfAttention, _require_2d_padding_mask
+    from disentangled_flash.modeling import DebertaAttentionConfig
+
+    config = DebertaAttentionConfig(hidden_size=64, num_attention_heads=2)
+    with pytest.raises(ValueError, match="fp32_precision"):
+        HipInferenceDisentangledSelfAttention(config, fp32_precision="tf32")
+    with pytest.raises(ValueError, match="relative_mode"):
+        HipInferenceDisentangledSelfAttention(config, relative_mode="dense")
+    module = HipInferenceDisentangledSelfAttention(config).eval()
+    module.prepare_for_inference(torch.randn(512, 64))
+    with torch.inference_mode(), pytest.raises(RuntimeError, match="GPU"):
+        module(torch.randn(1, 4, 64), torch.ones(1, 4))
+    with pytest.raises(ValueError, match="prepared on a GPU"):
+        module.prepare_shape(4, "cpu")
+    with pytest.raises(ValueError, match="factorized"):
+        _require_2d_padding_mask(torch.ones(1, 1, 4, 4), 1, 4)
+    with pytest.raises(ValueError, match="does not match"):
+        _require_2d_padding_mask(torch.ones(2, 4), 1, 4)
+
+
+def _tiny_deberta(layers=2, conv=3):
+    from transformers import DebertaV2Config, DebertaV2Model
+
+    config = DebertaV2Config(
+        vocab_size=100, hidden_size=64, num_hidden_layers=layers, num_attention_heads=2,
+        intermediate_size=128, hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0,
+        max_position_embeddings=64, type_vocab_size=0, relative_attention=True,
+        position_buckets=16, max_relative_positions=-1, pos_att_type=["p2c", "c2p"],
+        norm_rel_ebd="layer_norm", share_att_key=True, conv_kernel_size=conv,
+        conv_act="gelu", position_biased_input=False,
+    )
+    torch.manual_seed(0)
+    return DebertaV2Model(config).eval()
+
+
+@pytest.mark.parametrize("backend", ["torch", "optimized"])
+def test_encoder_torch_backend_matches_huggingface(backend):
+    from disentangled_flash import DebertaV2InferenceEncoder, enable_deberta_inference
+
+    model = _tiny_deberta().double()
+    fast = enable_deberta_inference(copy.deepcopy(model), backend=backend,
+                                    sequence_lengths=[24, 40])
+    assert isinstance(fast.encoder, DebertaV2InferenceEncoder)
+    assert set(fast.state_dict()) == set(model.state_dict())
+    ids = torch.randint(1, 100, (3, 40))
+    mask = (torch.arange(40)[None] < torch.tensor([[40], [23], [5]])).long()
+    with torch.inference_mode():
+        expected = model(input_ids=ids, attention_mask=mask).last_hidden_state
+        fast.encoder.activate_shape(40)
+        got = fast(input_ids=ids, attention_mask=mask).last_hidden_state
+    torch.testing.assert_close(got, expected, atol=1e-9, rtol=0)
+
+
+def test_encoder_api_errors():
+    from disentangled_flash import enable_deberta_inference
+    from disentangled_flash.deberta import resolve_backend
+
+    assert resolve_backend("triton") == "hip" and resolve_backend("optimized") == "torch"
+    with pytest.raises(ValueError, match="backend"):
+        resolve_backend("cuda")
+    model = _tiny_deberta(layers=1, conv=0)
+    with pytest.raises(TypeError):
+        enable_deberta_inference(torch.nn.Linear(2, 2))
+    enable_deberta_inference(model, backend="torch", sequence_lengths=[16])
+    with pytest.raises(TypeError, match="already"):
+        enable_deberta_inference(model, backend="torch")
+    encoder = model.encoder
+    with pytest.raises(ValueError, match="not prepared"):
+        encoder.activate_shape(32)
+    h = torch.randn(2, 16, 64)
+    with torch.inference_mode():
+        with pytest.raises(ValueError, match=r"\[B, L\]"):
+            encoder(h, torch.ones(2, 1, 16, 16))
+        with pytest.raises(ValueError, match="active bucket"):
+            encoder(torch.randn(2, 8, 64), torch.ones(2, 8))
+        with pytest.raises(ValueError, match="output_attentions"):
+            encoder(h, torch.ones(2, 16), output_attentions=True)
+    with pytest.raises(RuntimeError, match="no_grad"):
+        encoder(h, torch.ones(2, 16))
+    trained = _tiny_deberta(layers=1, conv=0).train()
+    with pytest.raises(RuntimeError, match="eval"):
+        enable_deberta_inference(trained, backend="torch", sequence_lengths=[8])
+
+
+def test_c_abi_library_exports_every_header_symbol():
+    import ctypes
+
+    from disentangled_flash import _lib
+
+    path = _lib.library_path()
+    if not path.exists():
+        pytest.skip("libdflash.so not built (run python __graft_entry__.py)")
+    header = (REPO / "include" / "dflash.h").read_text()
+    declared = re.findall(r"DFLASH_API\s+[\w\s\*]+?\b(dflash_\w+)\s*\(", header)
+    assert {"dflash_attention_fwd", "dflash_attention_rel_fwd", "dflash_error_string",
+            "dflash_abi_version"} <= set(declared)
+    lib = ctypes.CDLL(str(path))
+    for name in declared:
+        assert hasattr(lib, name), name
+    loaded = _lib.load()
+    assert loaded.dflash_abi_version() == _lib.ABI_VERSION
+    assert b"success" == loaded.dflash_error_string(0)
+
+
+def test_no_product_module_imports_the_oracle():
+    package = REPO / "disentangled-flash_amd"
+    for path in list(package.rglob("*.py")) + list(package.rglob("*.hip")):
+        text = path.read_text()
+        assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", text, re.M), path
