@@ -292,6 +292,10 @@ def main() -> int:
     parser.add_argument("--encoder-steps", type=int, default=20)
     parser.add_argument("--skip-encoder", action="store_true")
     parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--kernel-only", action="store_true",
+                        help="launch only the fused C2 kernel --steps times (profiling driver)")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="one 256 MiB device-to-device copy (HBM counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
@@ -307,6 +311,24 @@ def main() -> int:
     _lib.load()
     torch.backends.cuda.matmul.allow_tf32 = False
     log(f"device: {torch.cuda.get_device_name(0)}")
+
+    if args.copy_calibration:
+        src = torch.ones(128 * 1024 * 1024, dtype=torch.float16, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {src.numel() * src.element_size()} bytes")
+        return 0
+    if args.kernel_only:
+        inp = c2_inputs(torch.float16, padded=False)
+        call = fused_call(inp)
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            call()
+        torch.cuda.synchronize()
+        log(f"launched the fused C2 kernel {args.steps} times")
+        return 0
 
     # ---- headline: fused fp16 attention, C2 without padding (every FLOP real) ----
     full = c2_inputs(torch.float16, padded=False)
