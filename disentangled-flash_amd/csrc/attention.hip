@@ -33,205 +33,14 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "dflash.h"
 
+#include "device_common.h"
+#include "rel_attention.h"
+
 namespace dflash {
-
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kWaves = 4;               // wavefronts per workgroup
-constexpr int kThreads = kWaves * 64;
-
-// ---------------------------------------------------------------------------
-// MFMA wrappers.  A operand: lane l holds row l%16, k-slice l/16.  B operand:
-// lane l holds column l%16, the same k-slice.  C/D: lane l holds column l%16,
-// rows 4*(l/16) + r for r in 0..3.  The order of k inside a slice is the same
-// for A and B, so the products pair up whatever the hardware order is.
-// ---------------------------------------------------------------------------
-template <typename T>
-struct Mma;
-
-template <>
-struct Mma<_Float16> {
-  using frag = half8_t;
-  static constexpr int K = 32;     // k per instruction
-  static constexpr int PER = 8;    // elements of one lane's k-slice
-  __device__ static f32x4_t run(frag a, frag b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <>
-struct Mma<__bf16> {
-  using frag = bf16x8_t;
-  static constexpr int K = 32;
-  static constexpr int PER = 8;
-  __device__ static f32x4_t run(frag a, frag b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <>
-struct Mma<float> {
-  using frag = float;
-  static constexpr int K = 4;
-  static constexpr int PER = 1;
-  __device__ static f32x4_t run(frag a, frag b, f32x4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-  }
-};
-
-// Load one lane's k-slice starting at `base` (which already points at k0 of
-// the MFMA step for this lane's row/column).
-template <typename T>
-__device__ inline typename Mma<T>::frag load_slice(const T* base, int g) {
-  if constexpr (Mma<T>::PER == 8) {
-    return *reinterpret_cast<const typename Mma<T>::frag*>(base + 8 * g);
-  } else {
-    return base[g];
-  }
-}
-
-template <typename T>
-__device__ inline typename Mma<T>::frag zero_frag() {
-  typename Mma<T>::frag z;
-  if constexpr (Mma<T>::PER == 8) {
-    for (int e = 0; e < 8; ++e) z[e] = static_cast<T>(0.0f);
-  } else {
-    z = 0.0f;
-  }
-  return z;
-}
-
-template <typename T>
-__device__ inline T to_t(float x) {
-  return static_cast<T>(x);
-}
-
-template <typename T>
-__device__ inline float to_f(T x) {
-  return static_cast<float>(x);
-}
-
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-// s + a + b for two relative scores stored in T.  For 16-bit T the pair is
-// packed into one register and added with a single dot2 against (1, 1): the
-// products are exact and the sum is accumulated in fp32, so this equals the
-// two fp32 additions of the widened values up to fp32 rounding.
-template <typename T>
-__device__ inline float add_pair(float s, T a, T b) {
-  if constexpr (sizeof(T) == 4) {
-    return s + a + b;
-  } else if constexpr (__is_same(T, _Float16)) {
-    const half2_t v = {a, b};
-    const half2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-    return __builtin_amdgcn_fdot2(v, one, s, false);
-  } else {
-    const bf16x2_t v = {a, b};
-    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-    return __builtin_amdgcn_fdot2_f32_bf16(v, one, s, false);
-  }
-}
-
-// 16-byte global/LDS chunk copy.
-struct alignas(16) Chunk {
-  uint32_t w[4];
-};
-
-struct Params {
-  const void* q;
-  const void* k;
-  const void* v;
-  int64_t sb, sh, sl;          // element strides of q/k/v: batch, head, position
-  const void* pos_key;         // [H, S, D] (windowed) or c2p table [B, H, L, S]
-  const void* pos_query;       // [H, S, D] (windowed) or p2c table [B, H, L, S]
-  const int32_t* lut;          // delta_to_local [2L-1]
-  const uint8_t* mask;         // [B, L], nonzero = kept
-  void* out;                   // [B, L, H*D]
-  int B, H, L, S;
-  int nqb;                     // query blocks per (b, h)
-  float scale_log2;            // log2(e) / sqrt(d * factor)
-};
-
-// Padded LDS row lengths (elements).  16-bit rows stay 16-byte aligned.
-template <typename T>
-constexpr int pad_of() {
-  return sizeof(T) == 2 ? 8 : 4;
-}
-constexpr int round16(int x) { return (x + 15) / 16 * 16; }
-
-template <typename T, int D, int BN, int QW>
-struct Layout {
-  static constexpr int kQueriesPerWave = QW;                     // query rows per wavefront
-  static constexpr int kBlockM = kWaves * QW;                    // query rows per workgroup
-  static constexpr int kPad = pad_of<T>();
-  static constexpr int KS_LD = D + kPad;                         // Ks[BN][KS_LD]
-  static constexpr int VT_LD = BN + 4;                           // Vt[D][VT_LD]
-  static constexpr int WP_MAX = round16(kBlockM + BN - 1);       // p2c window
-  static constexpr int PW_LD = WP_MAX + kPad;                    // Pw[BN][PW_LD]
-  static constexpr int WC_MAX = round16(kQueriesPerWave + BN - 1);  // c2p window
-  static constexpr int CW_LD = WC_MAX + kPad;                    // Cw[w][QW][CW_LD]
-  static constexpr int LW_N = kBlockM + BN;                      // lut window
-
-  static constexpr size_t ks_bytes = size_t(BN) * KS_LD * sizeof(T);
-  static constexpr size_t vt_bytes = size_t(D) * VT_LD * sizeof(T);
-  static constexpr size_t pw_bytes = size_t(BN) * PW_LD * sizeof(T);
-  static constexpr size_t cw_bytes = size_t(kWaves) * kQueriesPerWave * CW_LD * sizeof(T);
-  static constexpr size_t lw_bytes = size_t(LW_N) * sizeof(int32_t);
-  static constexpr size_t kb_bytes = size_t(BN) * sizeof(float);
-
-  // Offsets; Pw/Cw exist only for the windowed kernels.
-  static constexpr size_t ks_off = 0;
-  static constexpr size_t vt_off = ks_off + ks_bytes;
-  static constexpr size_t kb_off = vt_off + vt_bytes;
-  static constexpr size_t lw_off = kb_off + kb_bytes;
-  static constexpr size_t pw_off = lw_off + lw_bytes;
-  static constexpr size_t cw_off = pw_off + pw_bytes;
-
-  static constexpr size_t bytes(bool windowed) {
-    return windowed ? cw_off + cw_bytes : pw_off;
-  }
-};
-
-// Workgroup barrier that orders LDS traffic only.  __syncthreads() also waits
-// for every outstanding global load (vmcnt(0)), which would force the
-// next-tile prefetch to land at the first barrier; here global loads stay in
-// flight and are waited for where their registers are used.
-__device__ inline void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ inline int clampi(int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); }
-
-// Physical workgroup n runs on XCD n % 8.  Renumber so that the query blocks
-// of one (b, h) - which share K, V and the relative tables - land on the same
-// XCD and hit the same L2.
-__device__ inline int xcd_logical_block(int n, int total) {
-  constexpr int kXcds = 8;
-  int per = total / kXcds;
-  int rem = total % kXcds;
-  int xcd = n % kXcds;
-  int idx = n / kXcds;
-  return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
-}
-
-// Four consecutive elements of T: one 8-byte (16-bit T) or 16-byte (fp32) access.
-template <typename T>
-using Quad = T __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-template <typename T>
-__device__ inline void store_quad(T* dst, f32x4_t acc) {
-  Quad<T> q;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) q[r] = to_t<T>(acc[r]);
-  *reinterpret_cast<Quad<T>*>(dst) = q;
-}
 
 template <typename T, int D, int BN, int QW, bool C2P, bool P2C, bool TABLE>
 __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
@@ -885,6 +694,28 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
                             reinterpret_cast<uintptr_t>(pos_key) |
                             reinterpret_cast<uintptr_t>(pos_query);
   if (addr_or % 16 != 0) return DFLASH_ERR_ALIGN;
+  if (dtype != DFLASH_DTYPE_FP32 && !getenv("DFLASH_REL_V1")) {
+    RelParams rp{};
+    rp.q = query;
+    rp.k = key;
+    rp.v = value;
+    rp.sb = stride_b;
+    rp.sh = stride_h;
+    rp.sl = stride_l;
+    rp.pos_key = has_c2p ? pos_key : query;
+    rp.pos_query = has_p2c ? pos_query : key;
+    rp.lut = delta_to_local;
+    rp.mask = attention_mask;
+    rp.out = out;
+    rp.B = B;
+    rp.H = H;
+    rp.L = L;
+    rp.S = (has_c2p || has_p2c) ? S : 1;
+    rp.scale_log2 = score_scale_log2;
+    rp.has_c2p = has_c2p;
+    rp.has_p2c = has_p2c;
+    return launch_rel_attention_16bit(rp, D, dtype, static_cast<hipStream_t>(stream));
+  }
   Params prm{};
   prm.q = query;
   prm.k = key;

@@ -26,6 +26,8 @@ OUTPUT = PACKAGE_ROOT / "disentangled_flash" / "libdflash.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU instructions.
+# -unaligned-access-mode: keep the compiler from merging 2-byte LDS reads into
+# unaligned 8-byte ones, which stall the LDS pipeline on gfx950.
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -34,6 +36,7 @@ COMMON_FLAGS = [
     "-fvisibility=hidden",
     "-ffp-contract=fast",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xclang", "-target-feature", "-Xclang", "-unaligned-access-mode",
     f"-I{INCLUDE}",
 ]
 

@@ -1,0 +1,642 @@
+// Fused DeBERTa disentangled attention with in-kernel relative scores,
+// 16-bit inputs (fp16 / bf16), gfx950 (CDNA4).
+//
+// Scores of one (batch, head), query i, key j (kernel.py:196-345):
+//
+//   s(i, j) = Q_i.K_j + c2p(i, slot(i-j)) + p2c(j, slot(i-j))
+//   c2p(i, s) = Q_i.Kr[s],  p2c(j, s) = K_j.Qr[s]   (each rounded to the input
+//   dtype, as the reference's separate torch.matmul outputs are, kernel.py:577,583)
+//
+// Workgroup = 4 wavefronts = 4*QW query rows of one (b, h); every wavefront
+// keeps its QW query rows in registers and walks the keys in tiles of BN.
+//
+// Relative scores are computed per *delta* rather than per slot: for a tile
+// the deltas i-j form one contiguous range, so the wavefront builds
+//
+//   Cw[q][t] = Q_{i0w+q} . Kr[slot(dlo_w + t)]      (its own QW queries)
+//
+// and the workgroup shares
+//
+//   Pw[jr][t] = K_{j0+jr} . Qr[slot(dlo + t)]
+//
+// with MFMA, where the rows Kr[slot(.)] / Qr[slot(.)] are gathered through
+// delta_to_local while they are loaded from L2.  Element (i, j) of the tile
+// then sits at a window index that is a lane constant plus a compile-time
+// offset, so the score gathers are LDS reads with immediate offsets and no
+// lookup table is touched inside the tile.  The price is that deltas sharing
+// a bucket are multiplied more than once, which costs MFMA cycles, of which
+// this kernel has spare (its bound is VALU).
+//
+// Layout of the score tile: S^T = K.Q^T with v_mfma_f32_16x16x32_{f16,bf16},
+// so each lane holds one query column and four consecutive keys per 16x16
+// block; the probabilities are then already the B operand of O^T += V^T.P^T.
+// Row sums come from the same MFMA with an all-ones A operand, so no
+// cross-lane reduction is needed for them.
+//
+// Global reads go through buffer resources: an offset at or past the
+// resource's size returns zero, which clamps rows past L for free; lookup
+// indices of deltas outside [-(L-1), L-1] are clamped to the end of the table
+// and read as slot 0 (those elements are masked or belong to rows that are
+// never stored).  Offsets are never negative.
+//
+// Mask semantics (kernel.py:250-261): kept query & kept key -> score; padded
+// query in range -> uniform over in-range keys; kept query & padded key ->
+// excluded; query past L -> key 0 only (row never stored).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device_common.h"
+#include "dflash.h"
+#include "rel_attention.h"
+
+namespace dflash {
+
+namespace {
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, gfx9 family descriptor word 3
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), kBufferFlags);
+}
+
+__device__ inline u32x4_t load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ inline u32x2_t load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ inline uint32_t load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ inline uint8_t load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+template <typename T>
+__device__ inline typename Mma<T>::frag as_frag(u32x4_t v) {
+  return __builtin_bit_cast(typename Mma<T>::frag, v);
+}
+
+template <typename T>
+__device__ inline typename Mma<T>::frag ones_frag() {
+  typename Mma<T>::frag f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = static_cast<T>(1.0f);
+  return f;
+}
+
+// Four fp32 accumulators -> four T values in one 8-byte LDS store.
+template <typename T>
+__device__ inline void store4(T* dst, f32x4_t acc) {
+  Quad<T> q;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(acc[r]);
+  *reinterpret_cast<Quad<T>*>(dst) = q;
+}
+
+// s + a + b with a, b in T: one dot2 against (1, 1) (exact products, fp32 sum).
+template <typename T>
+__device__ inline float add2(float s, T a, T b) {
+  if constexpr (__is_same(T, _Float16)) {
+    const half2_t v = {a, b};
+    const half2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    return __builtin_amdgcn_fdot2(v, one, s, false);
+  } else {
+    const bf16x2_t v = {a, b};
+    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(v, one, s, false);
+  }
+}
+
+template <typename T, int D, int QW, int BN>
+struct RelLayout {
+  static constexpr int BM = kWaves * QW;                // query rows per workgroup
+  static constexpr int NCC = (QW + BN - 1 + 15) / 16;   // c2p window chunks per wavefront
+  static constexpr int NPC = (BM + BN - 1 + 15) / 16;   // p2c window chunks per workgroup
+  static constexpr int PU = (NPC + kWaves - 1) / kWaves;  // p2c chunks per wavefront
+  static constexpr int KS_LD = D + 8;                   // Ks[BN][KS_LD]
+  static constexpr int VT_LD = BN + 4;                  // Vt[D][VT_LD]
+  static constexpr int CW_LD = 16 * NCC + 8;            // Cw[wave][QW][CW_LD]
+  static constexpr int PW_LD = 16 * NPC + 8;            // Pw[BN][PW_LD]
+
+  static constexpr size_t ks_off = 0;
+  static constexpr size_t vt_off = ks_off + size_t(BN) * KS_LD * sizeof(T);
+  static constexpr size_t pw_off = vt_off + size_t(D) * VT_LD * sizeof(T);
+  static constexpr size_t cw_off = pw_off + size_t(BN) * PW_LD * sizeof(T);
+  static constexpr size_t bytes = cw_off + size_t(kWaves) * QW * CW_LD * sizeof(T);
+};
+
+}  // namespace
+
+template <typename T, int D, int QW, int BN, bool C2P, bool P2C>
+__global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p) {
+  using M = Mma<T>;
+  using F = typename M::frag;
+  using LY = RelLayout<T, D, QW, BN>;
+  constexpr int BM = LY::BM;
+  constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
+  constexpr int KB = BN / 16;           // 16-key blocks per tile
+  constexpr int DB = D / 16;            // 16-dim blocks of the output
+  constexpr int KD = D / 32;            // MFMA k-steps over the head dimension
+  constexpr int CPR = D / 8;            // 16-byte chunks per K row
+  constexpr int NKC = BN * CPR;                  // 16-byte K chunks per tile
+  constexpr int NCH = (NKC + kThreads - 1) / kThreads;
+  constexpr int VQD = D / 4;                     // 4-dim quads per V row
+  constexpr int NVBT = (BN / 4) * VQD;           // 4x4 V blocks per tile
+  constexpr int NVB = (NVBT + kThreads - 1) / kThreads;
+  constexpr int NCC = LY::NCC;
+  constexpr int PU = LY::PU;
+  constexpr int NPC = LY::NPC;
+  constexpr uint32_t ES = sizeof(T);
+  static_assert(BN % 32 == 0 && BN <= 64, "key tile must be 32 or 64 keys");
+  static_assert(QW % 16 == 0, "query rows per wavefront must be a multiple of 16");
+  static_assert(NKC % kThreads == 0 || NKC < kThreads, "K tile must split evenly over the workgroup");
+  static_assert(NVBT % kThreads == 0 || NVBT < kThreads, "V tile must split evenly over the workgroup");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* Ks = reinterpret_cast<T*>(smem + LY::ks_off);
+  T* Vt = reinterpret_cast<T*>(smem + LY::vt_off);
+  T* Pw = reinterpret_cast<T*>(smem + LY::pw_off);
+  T* Cw = reinterpret_cast<T*>(smem + LY::cw_off);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+
+  const int L = p.L;
+  const int m = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int bh = m / p.nqb;
+  const int qblk = m - bh * p.nqb;
+  const int b = bh / p.H;
+  const int h = bh - b * p.H;
+  const int i0 = qblk * BM;
+  const int i0w = i0 + wave * QW;
+  const uint32_t sl_bytes = static_cast<uint32_t>(p.sl) * ES;
+
+  // Buffer resources.  Rows past L read as zero; the bound is the end of row L-1.
+  const uint32_t head_bytes = (static_cast<uint32_t>(L - 1) * static_cast<uint32_t>(p.sl) + D) * ES;
+  const int64_t head_off = static_cast<int64_t>(b) * p.sb + static_cast<int64_t>(h) * p.sh;
+  const auto rq = make_rsrc(reinterpret_cast<const T*>(p.q) + head_off, head_bytes);
+  const auto rk = make_rsrc(reinterpret_cast<const T*>(p.k) + head_off, head_bytes);
+  const auto rv = make_rsrc(reinterpret_cast<const T*>(p.v) + head_off, head_bytes);
+  const auto rmask = make_rsrc(p.mask + static_cast<int64_t>(b) * L, static_cast<uint32_t>(L));
+  const uint32_t rel_bytes = static_cast<uint32_t>(p.S) * D * ES;
+  const auto rkr = make_rsrc(reinterpret_cast<const T*>(p.pos_key) + static_cast<int64_t>(h) * p.S * D,
+                             rel_bytes);
+  const auto rqr = make_rsrc(reinterpret_cast<const T*>(p.pos_query) + static_cast<int64_t>(h) * p.S * D,
+                             rel_bytes);
+  const auto rlut = make_rsrc(p.lut, static_cast<uint32_t>(2 * L - 1) * 4u);
+
+  // ---- queries: fragments stay in registers (B operand of K.Q^T and Kr.Q^T) ----
+  F qf[kQB][KD];
+  bool qkept[kQB];
+  bool qin[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int i = i0w + 16 * qb + c;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd)
+      qf[qb][kd] = as_frag<T>(load16(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
+    qin[qb] = i < L;
+    qkept[qb] = load1(rmask, static_cast<uint32_t>(i)) != 0;  // zero past L
+  }
+  bool wave_all_kept = true;
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) wave_all_kept = wave_all_kept && __all(qkept[qb]);
+
+  // ---- per-thread offsets of the K / V tile loads (add j0 * row stride per tile) ----
+  uint32_t koff[NCH];
+  uint32_t kls[NCH];
+#pragma unroll
+  for (int n = 0; n < NCH; ++n) {
+    const int t = tid + n * kThreads;
+    const int r = t / CPR;
+    const int cc = t - r * CPR;
+    koff[n] = static_cast<uint32_t>(r) * sl_bytes + cc * 16;
+    kls[n] = static_cast<uint32_t>(r * LY::KS_LD + cc * 8);
+  }
+  uint32_t voff[NVB];
+  uint32_t vls[NVB];
+#pragma unroll
+  for (int n = 0; n < NVB; ++n) {
+    const int t = tid + n * kThreads;
+    const int kq = t / VQD;
+    const int dq = t - kq * VQD;
+    voff[n] = static_cast<uint32_t>(4 * kq) * sl_bytes + dq * 4 * ES;
+    vls[n] = static_cast<uint32_t>(4 * dq * LY::VT_LD + 4 * kq);
+  }
+
+  // ---- relative windows ----
+  // Tile at key offset j0: the wavefront's c2p window starts at delta
+  // dlo_w = i0w - j0 - (BN - 1), the workgroup's p2c window at
+  // dlo = i0 - j0 - (BN - 1); chunk k of a window covers deltas
+  // [start + 16k, start + 16k + 15] and lane c loads the row of delta start + 16k + c.
+  // The next tile's windows start BN = 16 * kSlide deltas lower, so its chunk k
+  // is this tile's chunk k - kSlide:
+  //   * c2p: chunks >= kSlide of the next tile are this tile's chunks < kCarry;
+  //     their values (queries are fixed per wavefront) are kept in registers
+  //     and only kSlide new chunks are multiplied per tile;
+  //   * p2c: chunk pc belongs to wavefront pc % 4 and kSlide == 4, so every
+  //     wavefront keeps its rows: per tile it loads one new chunk (pc = wave)
+  //     and shifts the others up by 4 (the values depend on the keys and are
+  //     recomputed).
+  constexpr int kSlide = BN / 16;
+  constexpr int kCarry = NCC - kSlide;
+  static_assert(kSlide == kWaves, "p2c chunk ownership needs a window slide of kWaves chunks");
+  static_assert(kCarry >= 0 && NPC % kWaves == 0, "window geometry");
+  auto lut_c_index = [&](int j0, int ch) { return i0w - j0 - (BN - 1) + 16 * ch + c + L - 1; };
+  auto lut_p_index = [&](int j0, int u) {
+    return i0 - j0 - (BN - 1) + 16 * (wave + kWaves * u) + c + L - 1;
+  };
+  // Deltas outside [-(L-1), L-1] (index outside [0, 2L-2]) read as slot 0: the
+  // unsigned min sends negative and too-large indices to 2L-1, the first
+  // out-of-range entry of the buffer (a wrapped 32-bit offset is not reliably
+  // out of range once the compiler folds constants into the instruction offset).
+  const uint32_t lut_end = static_cast<uint32_t>(2 * L - 1);
+  auto lut_load = [&](int index) {
+    const uint32_t idx = min(static_cast<uint32_t>(index), lut_end);
+    return static_cast<int>(load4(rlut, idx * 4u));
+  };
+  const uint32_t sub = (8 * g) * ES;
+  auto row_frag = [&](__amdgpu_buffer_rsrc_t r, int slot, int kd) {
+    return as_frag<T>(load16(r, static_cast<uint32_t>(slot) * (D * ES) + 32 * kd * ES + sub));
+  };
+
+  int lutc[C2P ? kSlide : 1];   // next tile's new c2p chunks
+  int lutp = 0;                 // next tile's new p2c chunk (pc = wave)
+  F crow[C2P ? kSlide : 1][KD];  // rows of this tile's new c2p chunks
+  Quad<T> ccar[C2P && kCarry > 0 ? kCarry : 1][kQB];  // c2p values carried into chunks >= kSlide
+  F prow[P2C ? PU : 1][KD];     // rows of this wavefront's p2c chunks wave + 4u
+
+  // ---- prefetch registers (K, V, mask of the next tile) ----
+  u32x4_t pk[NCH];
+  u32x2_t pv[NVB][4];
+  uint8_t pmask = 0;
+  auto prefetch_kv = [&](int j0) {
+    const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
+#pragma unroll
+    for (int n = 0; n < NCH; ++n)
+      if (NKC >= kThreads || tid < NKC) pk[n] = load16(rk, koff[n] + jb);
+#pragma unroll
+    for (int n = 0; n < NVB; ++n)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        if (NVBT >= kThreads || tid < NVBT) pv[n][rr] = load8(rv, voff[n] + jb + rr * sl_bytes);
+    pmask = load1(rmask, static_cast<uint32_t>(j0 + lane));
+  };
+
+  // ---- prologue: full windows of tile 0 ----
+  if constexpr (C2P) {
+    int lc[NCC];
+#pragma unroll
+    for (int ch = 0; ch < NCC; ++ch) lc[ch] = lut_load(lut_c_index(0, ch));
+#pragma unroll
+    for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = row_frag(rkr, lc[ch], kd);
+#pragma unroll
+    for (int ch = 0; ch < kCarry; ++ch) {
+      F r0[KD];
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) r0[kd] = row_frag(rkr, lc[kSlide + ch], kd);
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+        f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) acc = M::run(r0[kd], qf[qb][kd], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ccar[ch][qb][r] = static_cast<T>(acc[r]);
+      }
+    }
+  }
+  if constexpr (P2C) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int lp = lut_load(lut_p_index(0, u));
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) prow[u][kd] = row_frag(rqr, lp, kd);
+    }
+  }
+  prefetch_kv(0);
+  if constexpr (C2P) {
+#pragma unroll
+    for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(BN, ch));
+  }
+  if constexpr (P2C) lutp = lut_load(lut_p_index(BN, 0));
+
+  // ---- accumulators ----
+  f32x4_t o[DB][kQB];
+  f32x4_t rs[kQB];  // row sums (all four entries equal)
+  float row_max[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    row_max[qb] = -INFINITY;
+    rs[qb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[db][qb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Lane-constant LDS bases of the score gathers.  Element (qb, kb, r) of the
+  // tile has c2p window index 16*qb + c - (16*kb + 4*g + r) + BN - 1 in the
+  // wavefront's window, and p2c index QW*wave + that in the workgroup's.
+  constexpr int kMinOff = -(16 * (KB - 1) + 3);
+  const T* cw_lane = Cw + (wave * QW + c) * LY::CW_LD + c - 4 * g + BN - 1 + kMinOff;
+  const T* pw_lane = Pw + 4 * g * LY::PW_LD + QW * wave + c - 4 * g + BN - 1 + kMinOff;
+  const float scale = p.scale_log2;
+  const F ones = ones_frag<T>();
+
+  for (int j0 = 0; j0 < L; j0 += BN) {
+    lds_barrier();  // every wavefront is done with the previous tile's LDS
+
+    // ---- stage K and V^T ----
+#pragma unroll
+    for (int n = 0; n < NCH; ++n)
+      if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
+#pragma unroll
+    for (int n = 0; n < NVB; ++n) {
+      if (NVBT < kThreads && tid >= NVBT) break;
+      Quad<T> rows[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) rows[rr] = __builtin_bit_cast(Quad<T>, pv[n][rr]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Quad<T> col;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) col[rr] = rows[rr][e];
+        *reinterpret_cast<Quad<T>*>(Vt + vls[n] + e * LY::VT_LD) = col;
+      }
+    }
+    const uint64_t kept_bits = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
+
+    // ---- c2p window: Cw[q][t] = Kr[slot(dlo_w + t)] . Q_q (private to the wavefront) ----
+    if constexpr (C2P) {
+      T* cw_w = Cw + wave * QW * LY::CW_LD;
+      Quad<T> next_car[kCarry > 0 ? kCarry : 1][kQB];
+#pragma unroll
+      for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) acc = M::run(crow[ch][kd], qf[qb][kd], acc);
+          Quad<T> v4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v4[r] = static_cast<T>(acc[r]);
+          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * ch + 4 * g) = v4;
+          if (ch < kCarry) next_car[ch][qb] = v4;
+        }
+#pragma unroll
+      for (int ch = 0; ch < kCarry; ++ch)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * (kSlide + ch) + 4 * g) =
+              ccar[ch][qb];
+          ccar[ch][qb] = next_car[ch][qb];
+        }
+    }
+    lds_barrier();  // K tile staged
+
+    // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
+    f32x4_t sc[KB][kQB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      F kf[KD];
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd)
+        kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + c) * LY::KS_LD + 32 * kd + 8 * g);
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+        f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) acc = M::run(kf[kd], qf[qb][kd], acc);
+        sc[kb][qb] = acc;
+      }
+      if constexpr (P2C) {
+#pragma unroll
+        for (int u = 0; u < PU; ++u) {
+          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) acc = M::run(prow[u][kd], kf[kd], acc);
+          store4<T>(Pw + (16 * kb + c) * LY::PW_LD + 16 * (wave + kWaves * u) + 4 * g, acc);
+        }
+      }
+    }
+
+    // ---- next tile: K, V, mask, new window rows (lookups loaded one tile ahead) ----
+    const int jn = j0 + BN;
+    if (jn < L) {
+      prefetch_kv(jn);
+      if constexpr (C2P) {
+#pragma unroll
+        for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = row_frag(rkr, lutc[ch], kd);
+      }
+      if constexpr (P2C) {
+#pragma unroll
+        for (int u = PU - 1; u > 0; --u)
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) prow[u][kd] = prow[u - 1][kd];
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) prow[0][kd] = row_frag(rqr, lutp, kd);
+      }
+      if constexpr (C2P) {
+#pragma unroll
+        for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(jn + BN, ch));
+      }
+      if constexpr (P2C) lutp = lut_load(lut_p_index(jn + BN, 0));
+    }
+    if constexpr (P2C) lds_barrier();  // p2c window complete
+
+    // ---- relative scores ----
+    if constexpr (C2P || P2C) {
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int off = 16 * (qb - kb) - r - kMinOff;
+            if constexpr (C2P && P2C) {
+              const T cv = cw_lane[16 * qb * LY::CW_LD + off];
+              const T pv2 = pw_lane[(16 * kb + r) * LY::PW_LD + off];
+              sc[kb][qb][r] = add2<T>(sc[kb][qb][r], cv, pv2);
+            } else if constexpr (C2P) {
+              sc[kb][qb][r] += static_cast<float>(cw_lane[16 * qb * LY::CW_LD + off]);
+            } else {
+              sc[kb][qb][r] += static_cast<float>(pw_lane[(16 * kb + r) * LY::PW_LD + off]);
+            }
+          }
+    }
+
+    // ---- masking (wavefront-uniform slow path) ----
+    const bool full_tile = (j0 + BN <= L) && (BN == 64 ? kept_bits == ~uint64_t{0}
+                                                       : (kept_bits & ((uint64_t{1} << BN) - 1)) ==
+                                                             ((uint64_t{1} << BN) - 1));
+    if (!(full_tile && wave_all_kept)) {
+      const uint64_t lane_bits = kept_bits >> (4 * g);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = j0 + 16 * kb + 4 * g + r;
+          const bool key_kept = (lane_bits >> (16 * kb + r)) & 1;
+#pragma unroll
+          for (int qb = 0; qb < kQB; ++qb) {
+            // kept row: drop padded keys; padded row: uniform over in-range
+            // keys; row past L: key 0 only.
+            const bool hit = qkept[qb] ? key_kept : (qin[qb] ? j < L : j == 0);
+            const float v = qkept[qb] ? sc[kb][qb][r] : 0.0f;
+            sc[kb][qb][r] = hit ? v : -INFINITY;
+          }
+        }
+    }
+
+    // ---- online softmax (exp2, stale maximum) ----
+    // The exponent base only has to be common to a row and keep exp2 finite,
+    // so the previous maximum is reused while no scaled score exceeds it by
+    // more than kSlack; only then is the maximum reduced across lanes and the
+    // accumulators rescaled.  Wavefront-uniform branch.
+    constexpr float kSlack = 8.0f;
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      float lane_max = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lane_max = fmaxf(lane_max, sc[kb][qb][r]);
+      const float lane_max_s = lane_max * scale;
+      if (__any(lane_max_s > row_max[qb] + kSlack)) {
+        float tile_max = fmaxf(lane_max_s, __shfl_xor(lane_max_s, 16));
+        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+        const float new_max = fmaxf(row_max[qb], tile_max);
+        const float old_base = row_max[qb] == -INFINITY ? 0.0f : row_max[qb];
+        const float new_base = new_max == -INFINITY ? 0.0f : new_max;
+        const float corr = __builtin_amdgcn_exp2f(old_base - new_base);
+        row_max[qb] = new_max;
+        rs[qb] *= corr;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db][qb] *= corr;
+      }
+      const float neg_base = row_max[qb] == -INFINITY ? 0.0f : -row_max[qb];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sc[kb][qb][r] = __builtin_amdgcn_exp2f(fmaf(sc[kb][qb][r], scale, neg_base));
+    }
+
+    // ---- O^T += V^T . P^T, row sums += 1 . P^T ----
+#pragma unroll
+    for (int ks = 0; ks < BN / 32; ++ks) {
+      F pf[kQB];
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pf[qb][r] = static_cast<T>(sc[2 * ks][qb][r]);
+          pf[qb][4 + r] = static_cast<T>(sc[2 * ks + 1][qb][r]);
+        }
+        rs[qb] = M::run(ones, pf[qb], rs[qb]);
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const T* vrow = Vt + (16 * db + c) * LY::VT_LD + 32 * ks + 4 * g;
+        const Quad<T> lo = *reinterpret_cast<const Quad<T>*>(vrow);
+        const Quad<T> hi = *reinterpret_cast<const Quad<T>*>(vrow + 16);
+        F a;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          a[r] = lo[r];
+          a[4 + r] = hi[r];
+        }
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
+      }
+    }
+  }
+
+  // ---- normalise and store [B, L, H*D] ----
+  T* outp = reinterpret_cast<T*>(p.out);
+  const int64_t row_stride = static_cast<int64_t>(p.H) * D;
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int i = i0w + 16 * qb + c;
+    if (i >= L) continue;
+    const float inv = 1.0f / rs[qb][0];
+    T* dst = outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + 4 * g;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      Quad<T> q;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(o[db][qb][r] * inv);
+      *reinterpret_cast<Quad<T>*>(dst + 16 * db) = q;
+    }
+  }
+}
+
+namespace {
+
+// Tile configuration per head dimension: query rows per wavefront and keys
+// per tile.  d=128 halves the query rows to stay within 256 registers at two
+// wavefronts per SIMD.
+template <int D>
+constexpr int rel_queries_per_wave() {
+  return D >= 128 ? 16 : 32;
+}
+template <int D>
+constexpr int rel_block_n() {
+  return 64;
+}
+
+template <typename T, int D, bool C2P, bool P2C>
+int launch_rel(const RelParams& base, hipStream_t stream) {
+  constexpr int QW = rel_queries_per_wave<D>();
+  constexpr int BN = rel_block_n<D>();
+  using LY = RelLayout<T, D, QW, BN>;
+  RelParams prm = base;
+  prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
+  auto kernel = rel_attention_kernel<T, D, QW, BN, C2P, P2C>;
+  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(LY::bytes));
+  if (err != hipSuccess) return static_cast<int>(err);
+  const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H;
+  if (blocks > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), LY::bytes,
+                     stream, prm);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <typename T, int D>
+int rel_modes(const RelParams& prm, hipStream_t stream) {
+  if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, true, true>(prm, stream);
+  if (prm.has_c2p) return launch_rel<T, D, true, false>(prm, stream);
+  if (prm.has_p2c) return launch_rel<T, D, false, true>(prm, stream);
+  return launch_rel<T, D, false, false>(prm, stream);
+}
+
+}  // namespace
+
+int launch_rel_attention_16bit(const RelParams& prm, int D, int dtype, hipStream_t stream) {
+#define DFLASH_REL_CASE(TYPE, DIM) \
+  if (D == DIM) return rel_modes<TYPE, DIM>(prm, stream);
+  if (dtype == DFLASH_DTYPE_FP16) {
+    DFLASH_REL_CASE(_Float16, 32) DFLASH_REL_CASE(_Float16, 64) DFLASH_REL_CASE(_Float16, 128)
+  } else if (dtype == DFLASH_DTYPE_BF16) {
+    DFLASH_REL_CASE(__bf16, 32) DFLASH_REL_CASE(__bf16, 64) DFLASH_REL_CASE(__bf16, 128)
+  } else {
+    return DFLASH_ERR_DTYPE;
+  }
+#undef DFLASH_REL_CASE
+  return DFLASH_ERR_HEAD_DIM;
+}
+
+}  // namespace dflash
