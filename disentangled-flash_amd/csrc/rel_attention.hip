@@ -28,8 +28,8 @@
 // this kernel has spare (its bound is VALU).
 //
 // Layout of the score tile: S^T = K.Q^T with v_mfma_f32_16x16x32_{f16,bf16},
-// so each lane holds one query column and four consecutive keys per 16x16
-// block; the probabilities are then already the B operand of O^T += V^T.P^T.
+// so each lane holds one query column and four keys per 16x16 block; the
+// probabilities are then already the B operand of O^T += V^T.P^T.
 // Row sums come from the same MFMA with an all-ones A operand, so no
 // cross-lane reduction is needed for them.
 //
@@ -113,6 +113,12 @@ __device__ inline float add2(float s, T a, T b) {
   }
 }
 
+// Key of MFMA row x within a 16-key block: x = 4a + b holds key a + 4b, so
+// lane (c, g) of a 16x16 score block holds keys g + 4r (r = 0..3) and one
+// gather instruction (fixed r) touches four adjacent keys.  V^T columns use the
+// same order, so P^T and V^T pair up in the PV product.
+__device__ constexpr int key_of(int x) { return (x & 3) * 4 + (x >> 2); }
+
 template <typename T, int D, int QW, int BN>
 struct RelLayout {
   static constexpr int BM = kWaves * QW;                // query rows per workgroup
@@ -121,8 +127,13 @@ struct RelLayout {
   static constexpr int PU = (NPC + kWaves - 1) / kWaves;  // p2c chunks per wavefront
   static constexpr int KS_LD = D + 8;                   // Ks[BN][KS_LD]
   static constexpr int VT_LD = BN + 4;                  // Vt[D][VT_LD]
-  static constexpr int CW_LD = 16 * NCC + 8;            // Cw[wave][QW][CW_LD]
-  static constexpr int PW_LD = 16 * NPC + 8;            // Pw[BN][PW_LD]
+  // Row strides (in elements) chosen for the LDS of gfx950 as measured: 32
+  // four-byte banks served per half-wavefront, a 2-byte read of two lanes in
+  // one dword is a broadcast.  With them the score gathers (lanes = 16 queries
+  // x 4 adjacent keys) are conflict-free and the 8-byte window stores take the
+  // minimum two passes per half-wavefront.
+  static constexpr int CW_LD = NCC == 5 ? 88 : 16 * NCC + 4;  // Cw[wave][QW][CW_LD]
+  static constexpr int PW_LD = 16 * NPC + 20;                 // Pw[BN][PW_LD]
 
   static constexpr size_t ks_off = 0;
   static constexpr size_t vt_off = ks_off + size_t(BN) * KS_LD * sizeof(T);
@@ -229,7 +240,9 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     const int t = tid + n * kThreads;
     const int kq = t / VQD;
     const int dq = t - kq * VQD;
-    voff[n] = static_cast<uint32_t>(4 * kq) * sl_bytes + dq * 4 * ES;
+    // Thread block kq of a 16-key group holds keys kq%4 + {0, 4, 8, 12}, which
+    // land in V^T columns 4*(kq%4) + {0..3} (see key_of below).
+    voff[n] = static_cast<uint32_t>(16 * (kq / 4) + kq % 4) * sl_bytes + dq * 4 * ES;
     vls[n] = static_cast<uint32_t>(4 * dq * LY::VT_LD + 4 * kq);
   }
 
@@ -288,7 +301,7 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     for (int n = 0; n < NVB; ++n)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        if (NVBT >= kThreads || tid < NVBT) pv[n][rr] = load8(rv, voff[n] + jb + rr * sl_bytes);
+        if (NVBT >= kThreads || tid < NVBT) pv[n][rr] = load8(rv, voff[n] + jb + 4 * rr * sl_bytes);
     pmask = load1(rmask, static_cast<uint32_t>(j0 + lane));
   };
 
@@ -344,11 +357,12 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   }
 
   // Lane-constant LDS bases of the score gathers.  Element (qb, kb, r) of the
-  // tile has c2p window index 16*qb + c - (16*kb + 4*g + r) + BN - 1 in the
-  // wavefront's window, and p2c index QW*wave + that in the workgroup's.
-  constexpr int kMinOff = -(16 * (KB - 1) + 3);
-  const T* cw_lane = Cw + (wave * QW + c) * LY::CW_LD + c - 4 * g + BN - 1 + kMinOff;
-  const T* pw_lane = Pw + 4 * g * LY::PW_LD + QW * wave + c - 4 * g + BN - 1 + kMinOff;
+  // tile (query 16*qb + c, key 16*kb + g + 4*r) has c2p window index
+  // 16*qb + c - (16*kb + g + 4*r) + BN - 1 in the wavefront's window, and p2c
+  // index QW*wave + that in the workgroup's.
+  constexpr int kMinOff = -(16 * (KB - 1) + 12);
+  const T* cw_lane = Cw + (wave * QW + c) * LY::CW_LD + c - g + BN - 1 + kMinOff;
+  const T* pw_lane = Pw + g * LY::PW_LD + QW * wave + c - g + BN - 1 + kMinOff;
   const float scale = p.scale_log2;
   const F ones = ones_frag<T>();
 
@@ -410,7 +424,7 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
       F kf[KD];
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd)
-        kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + c) * LY::KS_LD + 32 * kd + 8 * g);
+        kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
 #pragma unroll
       for (int qb = 0; qb < kQB; ++qb) {
         f32x4_t acc{0.f, 0.f, 0.f, 0.f};
@@ -424,7 +438,7 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
           f32x4_t acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kd = 0; kd < KD; ++kd) acc = M::run(prow[u][kd], kf[kd], acc);
-          store4<T>(Pw + (16 * kb + c) * LY::PW_LD + 16 * (wave + kWaves * u) + 4 * g, acc);
+          store4<T>(Pw + (16 * kb + key_of(c)) * LY::PW_LD + 16 * (wave + kWaves * u) + 4 * g, acc);
         }
       }
     }
@@ -463,31 +477,30 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int off = 16 * (qb - kb) - r - kMinOff;
+            const int off = 16 * (qb - kb) - 4 * r - kMinOff;
             if constexpr (C2P && P2C) {
               const T cv = cw_lane[16 * qb * LY::CW_LD + off];
-              const T pv2 = pw_lane[(16 * kb + r) * LY::PW_LD + off];
+              const T pv2 = pw_lane[(16 * kb + 4 * r) * LY::PW_LD + off];
               sc[kb][qb][r] = add2<T>(sc[kb][qb][r], cv, pv2);
             } else if constexpr (C2P) {
               sc[kb][qb][r] += static_cast<float>(cw_lane[16 * qb * LY::CW_LD + off]);
             } else {
-              sc[kb][qb][r] += static_cast<float>(pw_lane[(16 * kb + r) * LY::PW_LD + off]);
+              sc[kb][qb][r] += static_cast<float>(pw_lane[(16 * kb + 4 * r) * LY::PW_LD + off]);
             }
           }
     }
 
     // ---- masking (wavefront-uniform slow path) ----
-    const bool full_tile = (j0 + BN <= L) && (BN == 64 ? kept_bits == ~uint64_t{0}
-                                                       : (kept_bits & ((uint64_t{1} << BN) - 1)) ==
-                                                             ((uint64_t{1} << BN) - 1));
+    constexpr uint64_t kTileBits = BN == 64 ? ~uint64_t{0} : (uint64_t{1} << (BN % 64)) - 1;
+    const bool full_tile = (j0 + BN <= L) && (kept_bits & kTileBits) == kTileBits;
     if (!(full_tile && wave_all_kept)) {
-      const uint64_t lane_bits = kept_bits >> (4 * g);
+      const uint64_t lane_bits = kept_bits >> g;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int j = j0 + 16 * kb + 4 * g + r;
-          const bool key_kept = (lane_bits >> (16 * kb + r)) & 1;
+          const int j = j0 + 16 * kb + g + 4 * r;
+          const bool key_kept = (lane_bits >> (16 * kb + 4 * r)) & 1;
 #pragma unroll
           for (int qb = 0; qb < kQB; ++qb) {
             // kept row: drop padded keys; padded row: uniform over in-range
