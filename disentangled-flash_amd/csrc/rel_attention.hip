@@ -135,9 +135,11 @@ struct RelLayout {
   static constexpr int CW_LD = NCC == 5 ? 88 : 16 * NCC + 4;  // Cw[wave][QW][CW_LD]
   static constexpr int PW_LD = 16 * NPC + 20;                 // Pw[BN][PW_LD]
 
+  static constexpr int VT_SIZE = D * VT_LD;             // elements of one V^T buffer
+
   static constexpr size_t ks_off = 0;
   static constexpr size_t vt_off = ks_off + size_t(BN) * KS_LD * sizeof(T);
-  static constexpr size_t pw_off = vt_off + size_t(D) * VT_LD * sizeof(T);
+  static constexpr size_t pw_off = vt_off + 2 * size_t(VT_SIZE) * sizeof(T);
   static constexpr size_t cw_off = pw_off + size_t(BN) * PW_LD * sizeof(T);
   static constexpr size_t bytes = cw_off + size_t(kWaves) * QW * CW_LD * sizeof(T);
 };
@@ -305,7 +307,80 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     pmask = load1(rmask, static_cast<uint32_t>(j0 + lane));
   };
 
-  // ---- prologue: full windows of tile 0 ----
+  // ---- staging and window helpers ----
+  // V^T is double-buffered: tile n reads buffer n & 1 while tile n+1 is staged
+  // into the other one, so K/V of the next tile go to LDS right after the p2c
+  // barrier instead of behind a third barrier.
+  auto stage_kv = [&](T* vt) {
+#pragma unroll
+    for (int n = 0; n < NCH; ++n)
+      if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
+#pragma unroll
+    for (int n = 0; n < NVB; ++n) {
+      if (NVBT < kThreads && tid >= NVBT) break;
+      Quad<T> rows[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) rows[rr] = __builtin_bit_cast(Quad<T>, pv[n][rr]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Quad<T> col;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) col[rr] = rows[rr][e];
+        *reinterpret_cast<Quad<T>*>(vt + vls[n] + e * LY::VT_LD) = col;
+      }
+    }
+  };
+  // c2p window of a tile: the kSlide new chunks are multiplied from crow (the
+  // products stay in registers until the previous tile's gathers are done),
+  // the kCarry old ones come from ccar.
+  Quad<T> cnew[C2P ? kSlide : 1][kQB];
+  auto c2p_products = [&]() {
+    if constexpr (C2P) {
+#pragma unroll
+      for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) acc = M::run(crow[ch][kd], qf[qb][kd], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cnew[ch][qb][r] = static_cast<T>(acc[r]);
+        }
+    }
+  };
+  auto c2p_store = [&]() {
+    if constexpr (C2P) {
+      T* cw_w = Cw + wave * QW * LY::CW_LD;
+#pragma unroll
+      for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb)
+          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * ch + 4 * g) =
+              cnew[ch][qb];
+#pragma unroll
+      for (int ch = 0; ch < kCarry; ++ch)
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * (kSlide + ch) + 4 * g) =
+              ccar[ch][qb];
+          ccar[ch][qb] = cnew[ch][qb];
+        }
+    }
+  };
+  // Rows of the new c2p chunks of tile jt (lookups in lutc), then the lookups
+  // of tile jt + BN.
+  auto load_crow = [&](int jt) {
+    if constexpr (C2P) {
+#pragma unroll
+      for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = row_frag(rkr, lutc[ch], kd);
+#pragma unroll
+      for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(jt + BN, ch));
+    }
+  };
+
+  // ---- prologue: windows and K/V of tile 0 ----
   if constexpr (C2P) {
     int lc[NCC];
 #pragma unroll
@@ -328,6 +403,8 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
         for (int r = 0; r < 4; ++r) ccar[ch][qb][r] = static_cast<T>(acc[r]);
       }
     }
+#pragma unroll
+    for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(BN, ch));
   }
   if constexpr (P2C) {
 #pragma unroll
@@ -336,13 +413,16 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) prow[u][kd] = row_frag(rqr, lp, kd);
     }
+    lutp = lut_load(lut_p_index(BN, 0));
   }
   prefetch_kv(0);
-  if constexpr (C2P) {
-#pragma unroll
-    for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(BN, ch));
-  }
-  if constexpr (P2C) lutp = lut_load(lut_p_index(BN, 0));
+  stage_kv(Vt);
+  uint64_t kept_cur = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
+  uint64_t kept_next = 0;
+  c2p_products();
+  c2p_store();
+  prefetch_kv(BN);
+  load_crow(BN);
 
   // ---- accumulators ----
   f32x4_t o[DB][kQB];
@@ -366,56 +446,13 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   const float scale = p.scale_log2;
   const F ones = ones_frag<T>();
 
+  // Per tile: barrier B (K/V staged, previous gathers done) -> QK, p2c window;
+  // barrier C (p2c window complete, K tile consumed) -> stage the next K/V,
+  // gathers, softmax, PV, next c2p window.
+  int vbuf = 0;
   for (int j0 = 0; j0 < L; j0 += BN) {
-    lds_barrier();  // every wavefront is done with the previous tile's LDS
-
-    // ---- stage K and V^T ----
-#pragma unroll
-    for (int n = 0; n < NCH; ++n)
-      if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
-#pragma unroll
-    for (int n = 0; n < NVB; ++n) {
-      if (NVBT < kThreads && tid >= NVBT) break;
-      Quad<T> rows[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) rows[rr] = __builtin_bit_cast(Quad<T>, pv[n][rr]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Quad<T> col;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) col[rr] = rows[rr][e];
-        *reinterpret_cast<Quad<T>*>(Vt + vls[n] + e * LY::VT_LD) = col;
-      }
-    }
-    const uint64_t kept_bits = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
-
-    // ---- c2p window: Cw[q][t] = Kr[slot(dlo_w + t)] . Q_q (private to the wavefront) ----
-    if constexpr (C2P) {
-      T* cw_w = Cw + wave * QW * LY::CW_LD;
-      Quad<T> next_car[kCarry > 0 ? kCarry : 1][kQB];
-#pragma unroll
-      for (int ch = 0; ch < kSlide; ++ch)
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kd = 0; kd < KD; ++kd) acc = M::run(crow[ch][kd], qf[qb][kd], acc);
-          Quad<T> v4;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) v4[r] = static_cast<T>(acc[r]);
-          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * ch + 4 * g) = v4;
-          if (ch < kCarry) next_car[ch][qb] = v4;
-        }
-#pragma unroll
-      for (int ch = 0; ch < kCarry; ++ch)
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * (kSlide + ch) + 4 * g) =
-              ccar[ch][qb];
-          ccar[ch][qb] = next_car[ch][qb];
-        }
-    }
-    lds_barrier();  // K tile staged
+    const int jn = j0 + BN;
+    lds_barrier();
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
     f32x4_t sc[KB][kQB];
@@ -442,32 +479,27 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
         }
       }
     }
-
-    // ---- next tile: K, V, mask, new window rows (lookups loaded one tile ahead) ----
-    const int jn = j0 + BN;
-    if (jn < L) {
-      prefetch_kv(jn);
-      if constexpr (C2P) {
+    if constexpr (P2C) {
+      // Next tile's p2c rows: shift the kept chunks up by 4, load the new one.
 #pragma unroll
-        for (int ch = 0; ch < kSlide; ++ch)
+      for (int u = PU - 1; u > 0; --u)
 #pragma unroll
-          for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = row_frag(rkr, lutc[ch], kd);
-      }
-      if constexpr (P2C) {
+        for (int kd = 0; kd < KD; ++kd) prow[u][kd] = prow[u - 1][kd];
 #pragma unroll
-        for (int u = PU - 1; u > 0; --u)
-#pragma unroll
-          for (int kd = 0; kd < KD; ++kd) prow[u][kd] = prow[u - 1][kd];
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd) prow[0][kd] = row_frag(rqr, lutp, kd);
-      }
-      if constexpr (C2P) {
-#pragma unroll
-        for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(jn + BN, ch));
-      }
-      if constexpr (P2C) lutp = lut_load(lut_p_index(jn + BN, 0));
+      for (int kd = 0; kd < KD; ++kd) prow[0][kd] = row_frag(rqr, lutp, kd);
+      lutp = lut_load(lut_p_index(jn + BN, 0));
     }
-    if constexpr (P2C) lds_barrier();  // p2c window complete
+    lds_barrier();
+
+    // ---- stage the next tile; its c2p products overlap this tile's softmax ----
+    // Next-tile work runs unconditionally (no branch splits the scheduling
+    // region): past the last tile the buffer loads read zeros and the LDS
+    // writes land in buffers nothing reads any more.
+    const T* vt_cur = Vt + vbuf * LY::VT_SIZE;
+    stage_kv(Vt + (vbuf ^ 1) * LY::VT_SIZE);
+    kept_next = __ballot(pmask != 0);
+    prefetch_kv(jn + BN);
+    c2p_products();
 
     // ---- relative scores ----
     if constexpr (C2P || P2C) {
@@ -492,9 +524,9 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
 
     // ---- masking (wavefront-uniform slow path) ----
     constexpr uint64_t kTileBits = BN == 64 ? ~uint64_t{0} : (uint64_t{1} << (BN % 64)) - 1;
-    const bool full_tile = (j0 + BN <= L) && (kept_bits & kTileBits) == kTileBits;
+    const bool full_tile = (j0 + BN <= L) && (kept_cur & kTileBits) == kTileBits;
     if (!(full_tile && wave_all_kept)) {
-      const uint64_t lane_bits = kept_bits >> g;
+      const uint64_t lane_bits = kept_cur >> g;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -561,7 +593,7 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const T* vrow = Vt + (16 * db + c) * LY::VT_LD + 32 * ks + 4 * g;
+        const T* vrow = vt_cur + (16 * db + c) * LY::VT_LD + 32 * ks + 4 * g;
         const Quad<T> lo = *reinterpret_cast<const Quad<T>*>(vrow);
         const Quad<T> hi = *reinterpret_cast<const Quad<T>*>(vrow + 16);
         F a;
@@ -574,6 +606,12 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
         for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
       }
     }
+
+    // ---- next tile's c2p window (after this tile's gathers), its next rows ----
+    c2p_store();
+    load_crow(jn + BN);
+    kept_cur = kept_next;
+    vbuf ^= 1;
   }
 
   // ---- normalise and store [B, L, H*D] ----
