@@ -550,6 +550,8 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     // more than kSlack; only then is the maximum reduced across lanes and the
     // accumulators rescaled.  Wavefront-uniform branch.
     constexpr float kSlack = 8.0f;
+    float lane_max_s[kQB];
+    bool grow = false;
 #pragma unroll
     for (int qb = 0; qb < kQB; ++qb) {
       float lane_max = -INFINITY;
@@ -557,9 +559,15 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) lane_max = fmaxf(lane_max, sc[kb][qb][r]);
-      const float lane_max_s = lane_max * scale;
-      if (__any(lane_max_s > row_max[qb] + kSlack)) {
-        float tile_max = fmaxf(lane_max_s, __shfl_xor(lane_max_s, 16));
+      lane_max_s[qb] = lane_max * scale;
+      grow = grow || lane_max_s[qb] > row_max[qb] + kSlack;
+    }
+    // One wavefront-uniform branch for all query blocks, so that the common
+    // path (no rescale) is a single scheduling region.
+    if (__any(grow)) {
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+        float tile_max = fmaxf(lane_max_s[qb], __shfl_xor(lane_max_s[qb], 16));
         tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
         const float new_max = fmaxf(row_max[qb], tile_max);
         const float old_base = row_max[qb] == -INFINITY ? 0.0f : row_max[qb];
@@ -570,6 +578,9 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
 #pragma unroll
         for (int db = 0; db < DB; ++db) o[db][qb] *= corr;
       }
+    }
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
       const float neg_base = row_max[qb] == -INFINITY ? 0.0f : -row_max[qb];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
