@@ -1,0 +1,147 @@
+// Fused residual add + LayerNorm for the DeBERTa encoder layer outputs
+// (DebertaV2SelfOutput / DebertaV2Output: LayerNorm(dense(x) + input),
+// _reference.py:108-112, 482-485).
+//
+// One wavefront per row.  The sum dense + residual is rounded to the
+// activation dtype first, exactly as the separate elementwise add of the
+// reference produces it, then normalised in fp32 with a two-pass mean /
+// variance over the values held in registers:
+//
+//   s = T(x + r);  y = T((s - mean(s)) * rsqrt(var(s) + eps) * gamma + beta)
+//
+// HBM traffic per row: read x and r, write y (3 * H * sizeof(T) bytes), which
+// replaces the add's read-read-write plus the LayerNorm's read-write.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dflash.h"
+
+namespace dflash {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one wavefront per row
+
+template <typename T>
+struct Vec4 {
+  typedef T type __attribute__((ext_vector_type(4)));
+};
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// VPL = number of 4-element chunks per lane (H <= 256 * VPL).
+template <typename T, int VPL>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
+    const T* __restrict__ x, const T* __restrict__ r, const T* __restrict__ gamma,
+    const T* __restrict__ beta, T* __restrict__ y, int rows, int hidden, float eps) {
+  using V = typename Vec4<T>::type;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wavefronts exit together
+  const int64_t base = static_cast<int64_t>(row) * hidden;
+  const int nvec = hidden >> 2;
+
+  float s[VPL][4];
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + 64 * k;
+    if (v < nvec) {
+      const V a = *reinterpret_cast<const V*>(x + base + 4 * v);
+      const V b = *reinterpret_cast<const V*>(r + base + 4 * v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s[k][e] = static_cast<float>(static_cast<T>(static_cast<float>(a[e]) + static_cast<float>(b[e])));
+        sum += s[k][e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[k][e] = 0.0f;
+    }
+  }
+  const float inv_h = 1.0f / static_cast<float>(hidden);
+  const float mean = wave_sum(sum) * inv_h;
+  float sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    if (lane + 64 * k < nvec) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = s[k][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(sq) * inv_h + eps);
+#pragma unroll
+  for (int k = 0; k < VPL; ++k) {
+    const int v = lane + 64 * k;
+    if (v < nvec) {
+      const V g = *reinterpret_cast<const V*>(gamma + 4 * v);
+      const V bb = *reinterpret_cast<const V*>(beta + 4 * v);
+      V out;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        out[e] = static_cast<T>((s[k][e] - mean) * rstd * static_cast<float>(g[e]) +
+                                static_cast<float>(bb[e]));
+      *reinterpret_cast<V*>(y + base + 4 * v) = out;
+    }
+  }
+}
+
+template <typename T, int VPL>
+int launch_ln(const void* x, const void* r, const void* gamma, const void* beta, void* y,
+              int rows, int hidden, float eps, hipStream_t stream) {
+  const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+  hipLaunchKernelGGL((add_layernorm_kernel<T, VPL>), dim3(blocks), dim3(64 * kRowsPerBlock), 0,
+                     stream, static_cast<const T*>(x), static_cast<const T*>(r),
+                     static_cast<const T*>(gamma), static_cast<const T*>(beta),
+                     static_cast<T*>(y), rows, hidden, eps);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <typename T>
+int dispatch_ln(const void* x, const void* r, const void* gamma, const void* beta, void* y,
+                int rows, int hidden, float eps, hipStream_t stream) {
+  const int vpl = (hidden + 255) / 256;
+  switch (vpl) {
+    case 1: return launch_ln<T, 1>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+    case 2: return launch_ln<T, 2>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+    case 3: return launch_ln<T, 3>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+    case 4: return launch_ln<T, 4>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+    case 5:
+    case 6: return launch_ln<T, 6>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+    case 7:
+    case 8: return launch_ln<T, 8>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+    default: return launch_ln<T, 16>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  }
+}
+
+}  // namespace
+}  // namespace dflash
+
+using namespace dflash;
+
+extern "C" int dflash_add_layernorm_fwd(const void* x, const void* residual, const void* gamma,
+                                        const void* beta, void* out, int rows, int hidden,
+                                        float eps, int dtype, void* stream) {
+  if (rows < 0 || hidden < 4 || hidden % 4 != 0 || hidden > 4096) return DFLASH_ERR_SHAPE;
+  if (rows == 0) return DFLASH_OK;  // nothing to do; empty tensors may carry null pointers
+  if (!x || !residual || !gamma || !beta || !out) return DFLASH_ERR_NULL;
+  const int esize = dtype == DFLASH_DTYPE_FP32 ? 4 : 2;
+  const uintptr_t addr_or = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
+                            reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta) |
+                            reinterpret_cast<uintptr_t>(out);
+  if (addr_or % (4 * esize) != 0) return DFLASH_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case DFLASH_DTYPE_FP16: return dispatch_ln<_Float16>(x, residual, gamma, beta, out, rows, hidden, eps, s);
+    case DFLASH_DTYPE_BF16: return dispatch_ln<__bf16>(x, residual, gamma, beta, out, rows, hidden, eps, s);
+    case DFLASH_DTYPE_FP32: return dispatch_ln<float>(x, residual, gamma, beta, out, rows, hidden, eps, s);
+    default: return DFLASH_ERR_DTYPE;
+  }
+}

@@ -18,7 +18,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load torch's HIP runtime first)
 
 LIBRARY_NAME = "libdflash.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODES = {
     torch.float16: 0,
@@ -59,6 +59,12 @@ def _bind(lib: ctypes.CDLL) -> None:
         _c_int, _c_int, _c_int, _c_int, _c_int,      # B, H, L, D, S
         _c_float, _c_int, _c_int, _c_int, _c_int,    # scale, has_c2p, has_p2c, dtype, strict
         _c_void_p,                                   # stream
+    ]
+    lib.dflash_add_layernorm_fwd.restype = _c_int
+    lib.dflash_add_layernorm_fwd.argtypes = [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, residual, gamma, beta, out
+        _c_int, _c_int, _c_float, _c_int,                        # rows, hidden, eps, dtype
+        _c_void_p,                                               # stream
     ]
     lib.dflash_error_string.restype = ctypes.c_char_p
     lib.dflash_error_string.argtypes = [_c_int]

@@ -23,7 +23,7 @@ extern "C" {
 
 #define DFLASH_API __attribute__((visibility("default")))
 
-#define DFLASH_ABI_VERSION 1
+#define DFLASH_ABI_VERSION 2
 
 #define DFLASH_DTYPE_FP16 0
 #define DFLASH_DTYPE_BF16 1
@@ -86,6 +86,25 @@ DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, cons
                              void* out, int B, int H, int L, int D, int S,
                              float score_scale_log2, int has_c2p, int has_p2c, int dtype,
                              int strict_fp32, void* stream);
+
+/*
+ * Fused residual add + LayerNorm of an encoder layer output.
+ *
+ * Replaces the tail of DebertaV2SelfOutput.forward and DebertaV2Output.forward,
+ * LayerNorm(dense(x) + input_tensor)
+ * (/root/reference/src/disentangled_flash/_reference.py:108-112 and 482-485;
+ * the dropout between them is the identity in inference), for the encoder
+ * loop of DebertaV2InferenceEncoder.forward_prepared
+ * (/root/reference/src/disentangled_flash/deberta.py:262-276):
+ *   x, residual, out : [rows, hidden], dtype `dtype`, contiguous
+ *   gamma, beta      : [hidden], dtype `dtype` (the LayerNorm weight and bias)
+ *   out = LayerNorm(T(x + residual)) with eps, statistics in fp32.
+ * hidden must be a multiple of 4 and at most 4096; pointers 4-element aligned.
+ * rows == 0 is a no-op (pointers are not inspected).
+ */
+DFLASH_API int dflash_add_layernorm_fwd(const void* x, const void* residual, const void* gamma,
+                                        const void* beta, void* out, int rows, int hidden,
+                                        float eps, int dtype, void* stream);
 
 /* Text for a return code of any dflash_* entry point. */
 DFLASH_API const char* dflash_error_string(int code);

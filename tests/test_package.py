@@ -261,3 +261,21 @@ def test_no_product_module_imports_the_oracle():
     for path in list(package.rglob("*.py")) + list(package.rglob("*.hip")):
         text = path.read_text()
         assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", text, re.M), path
+
+
+def test_fusable_output_block_rules():
+    from torch import nn
+    from transformers import DebertaV2Config
+    from transformers.models.deberta_v2.modeling_deberta_v2 import DebertaV2SelfOutput
+
+    from disentangled_flash.layers import fusable_output_block
+
+    cfg = DebertaV2Config(hidden_size=64, intermediate_size=128, hidden_dropout_prob=0.0)
+    block = DebertaV2SelfOutput(cfg)
+    assert fusable_output_block(block)
+    block.dense = nn.Linear(64, 64, bias=False)
+    assert not fusable_output_block(block)
+    other = DebertaV2SelfOutput(cfg)
+    other.LayerNorm = nn.LayerNorm(64, elementwise_affine=False)
+    assert not fusable_output_block(other)
+    assert not fusable_output_block(nn.Linear(4, 4))
