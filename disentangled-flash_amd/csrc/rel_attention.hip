@@ -351,18 +351,24 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   auto c2p_store = [&]() {
     if constexpr (C2P) {
       T* cw_w = Cw + wave * QW * LY::CW_LD;
+      // Queries of block qb meet window indices [16qb, 16qb + BN + 14]: chunks
+      // outside [qb, qb + KB] are not stored (they are still multiplied when a
+      // later tile needs them as carried chunks).
+      auto needed = [](int ch, int qb) { return ch >= qb && ch <= qb + KB; };
 #pragma unroll
       for (int ch = 0; ch < kSlide; ++ch)
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb)
-          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * ch + 4 * g) =
-              cnew[ch][qb];
+          if (needed(ch, qb))
+            *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * ch + 4 * g) =
+                cnew[ch][qb];
 #pragma unroll
       for (int ch = 0; ch < kCarry; ++ch)
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
-          *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * (kSlide + ch) + 4 * g) =
-              ccar[ch][qb];
+          if (needed(kSlide + ch, qb))
+            *reinterpret_cast<Quad<T>*>(cw_w + (16 * qb + c) * LY::CW_LD + 16 * (kSlide + ch) + 4 * g) =
+                ccar[ch][qb];
           ccar[ch][qb] = cnew[ch][qb];
         }
     }
@@ -470,12 +476,16 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
         sc[kb][qb] = acc;
       }
       if constexpr (P2C) {
+        // Keys of block kb meet window indices [BN - 16(kb+1), BM + BN - 2 - 16kb]:
+        // chunks outside [KB-1-kb, (BM+BN-2)/16 - kb] are read by no score element.
 #pragma unroll
         for (int u = 0; u < PU; ++u) {
+          const int pc = wave + kWaves * u;
+          if (pc < KB - 1 - kb || pc > (BM + BN - 2) / 16 - kb) continue;
           f32x4_t acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int kd = 0; kd < KD; ++kd) acc = M::run(prow[u][kd], kf[kd], acc);
-          store4<T>(Pw + (16 * kb + key_of(c)) * LY::PW_LD + 16 * (wave + kWaves * u) + 4 * g, acc);
+          store4<T>(Pw + (16 * kb + key_of(c)) * LY::PW_LD + 16 * pc + 4 * g, acc);
         }
       }
     }
