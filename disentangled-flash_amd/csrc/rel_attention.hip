@@ -41,7 +41,9 @@
 //
 // Mask semantics (kernel.py:250-261): kept query & kept key -> score; padded
 // query in range -> uniform over in-range keys; kept query & padded key ->
-// excluded; query past L -> key 0 only (row never stored).
+// excluded; query past L -> first visited key only (row never stored).  The
+// key loop of a workgroup visits only the tiles between the first and last kept
+// key of the sequence; padded rows are stored as the mean of V.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -224,6 +226,98 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) wave_all_kept = wave_all_kept && __all(qkept[qb]);
 
+  // ---- padding extent (wavefront-uniform; every wavefront derives the same values) ----
+  // A kept query attends to kept keys only, so the key loop of a workgroup
+  // with kept queries is trimmed to the 64-key tiles from the first to the
+  // last kept key of the sequence.  A padded query in range attends uniformly
+  // to all L keys: its output is the mean of V over the sequence, which does
+  // not depend on the query and is computed separately (v_mean below).
+  bool wg_kept = false;
+  bool wg_padded = false;
+#pragma unroll
+  for (int q0 = 0; q0 < BM; q0 += 64) {
+    const int i = i0 + q0 + lane;
+    const bool mine = q0 + lane < BM;
+    const bool kept = mine && load1(rmask, static_cast<uint32_t>(i)) != 0;
+    wg_kept = wg_kept || __any(kept);
+    wg_padded = wg_padded || __any(mine && i < L && !kept);
+  }
+  int kfirst = 0;
+  int klast = L - 1;
+  if (wg_kept) {
+    kfirst = L;
+    klast = -1;
+    for (int base = 0; base < L; base += 256) {
+      uint8_t km[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) km[e] = load1(rmask, static_cast<uint32_t>(base + 64 * e + lane));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t bits = __ballot(km[e] != 0);
+        if (bits != 0) {
+          kfirst = min(kfirst, base + 64 * e + __builtin_ctzll(bits));
+          klast = max(klast, base + 64 * e + 63 - __builtin_clzll(bits));
+        }
+      }
+    }
+  }
+  const int jstart = (kfirst / BN) * BN;
+  const int jend = klast + 1;
+
+  // Mean of V over the L keys of (b, h) in fp32, left in LDS at vmean[0..D).
+  float* vred = reinterpret_cast<float*>(smem);
+  float* vmean = vred + kThreads * 8;
+  auto v_mean = [&]() {
+    constexpr int RG = kThreads / CPR;  // rows summed in parallel
+    const int cc = tid % CPR;
+    const int rg = tid / CPR;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    auto add_row = [&](u32x4_t raw) {
+      const F v = as_frag<T>(raw);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
+    };
+    int j = rg;
+    for (; j + 3 * RG < L; j += 4 * RG) {
+      u32x4_t raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) raw[u] = load16(rv, static_cast<uint32_t>(j + u * RG) * sl_bytes + cc * 16);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) add_row(raw[u]);
+    }
+    for (; j < L; j += RG) add_row(load16(rv, static_cast<uint32_t>(j) * sl_bytes + cc * 16));
+    lds_barrier();  // LDS of the key loop no longer read
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vred[tid * 8 + e] = acc[e];
+    lds_barrier();
+    if (tid < D) {
+      const int col = tid >> 3;
+      const int e = tid & 7;
+      float s = 0.0f;
+      for (int r = 0; r < RG; ++r) s += vred[(r * CPR + col) * 8 + e];
+      vmean[tid] = s / static_cast<float>(L);
+    }
+    lds_barrier();
+  };
+
+  T* outp = reinterpret_cast<T*>(p.out);
+  const int64_t row_stride = static_cast<int64_t>(p.H) * D;
+  if (!wg_kept) {
+    // Every query of the workgroup is padded (or past L): all rows are the mean of V.
+    v_mean();
+    const int row_lo = i0 + tid / (D / 4);
+    for (int i = row_lo; i < min(i0 + BM, L); i += kThreads / (D / 4)) {
+      const int d0 = 4 * (tid % (D / 4));
+      Quad<T> q;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[d0 + r]);
+      *reinterpret_cast<Quad<T>*>(outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + d0) = q;
+    }
+    return;
+  }
+
   // ---- per-thread offsets of the K / V tile loads (add j0 * row stride per tile) ----
   uint32_t koff[NCH];
   uint32_t kls[NCH];
@@ -390,7 +484,7 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   if constexpr (C2P) {
     int lc[NCC];
 #pragma unroll
-    for (int ch = 0; ch < NCC; ++ch) lc[ch] = lut_load(lut_c_index(0, ch));
+    for (int ch = 0; ch < NCC; ++ch) lc[ch] = lut_load(lut_c_index(jstart, ch));
 #pragma unroll
     for (int ch = 0; ch < kSlide; ++ch)
 #pragma unroll
@@ -410,25 +504,25 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
       }
     }
 #pragma unroll
-    for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(BN, ch));
+    for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(jstart + BN, ch));
   }
   if constexpr (P2C) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) {
-      const int lp = lut_load(lut_p_index(0, u));
+      const int lp = lut_load(lut_p_index(jstart, u));
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) prow[u][kd] = row_frag(rqr, lp, kd);
     }
-    lutp = lut_load(lut_p_index(BN, 0));
+    lutp = lut_load(lut_p_index(jstart + BN, 0));
   }
-  prefetch_kv(0);
+  prefetch_kv(jstart);
   stage_kv(Vt);
   uint64_t kept_cur = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
   uint64_t kept_next = 0;
   c2p_products();
   c2p_store();
-  prefetch_kv(BN);
-  load_crow(BN);
+  prefetch_kv(jstart + BN);
+  load_crow(jstart + BN);
 
   // ---- accumulators ----
   f32x4_t o[DB][kQB];
@@ -456,7 +550,7 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   // barrier C (p2c window complete, K tile consumed) -> stage the next K/V,
   // gathers, softmax, PV, next c2p window.
   int vbuf = 0;
-  for (int j0 = 0; j0 < L; j0 += BN) {
+  for (int j0 = jstart; j0 < jend; j0 += BN) {
     const int jn = j0 + BN;
     lds_barrier();
 
@@ -546,8 +640,9 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
 #pragma unroll
           for (int qb = 0; qb < kQB; ++qb) {
             // kept row: drop padded keys; padded row: uniform over in-range
-            // keys; row past L: key 0 only.
-            const bool hit = qkept[qb] ? key_kept : (qin[qb] ? j < L : j == 0);
+            // keys (replaced by the mean of V at the end); row past L: the
+            // first visited key only (never stored).
+            const bool hit = qkept[qb] ? key_kept : (qin[qb] ? j < L : j == jstart);
             const float v = qkept[qb] ? sc[kb][qb][r] : 0.0f;
             sc[kb][qb][r] = hit ? v : -INFINITY;
           }
@@ -635,9 +730,8 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     vbuf ^= 1;
   }
 
-  // ---- normalise and store [B, L, H*D] ----
-  T* outp = reinterpret_cast<T*>(p.out);
-  const int64_t row_stride = static_cast<int64_t>(p.H) * D;
+  // ---- normalise and store [B, L, H*D]; padded rows take the mean of V ----
+  if (wg_padded) v_mean();
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     const int i = i0w + 16 * qb + c;
@@ -647,8 +741,13 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       Quad<T> q;
+      if (qkept[qb]) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(o[db][qb][r] * inv);
+        for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(o[db][qb][r] * inv);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[16 * db + 4 * g + r]);
+      }
       *reinterpret_cast<Quad<T>*>(dst + 16 * db) = q;
     }
   }

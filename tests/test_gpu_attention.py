@@ -37,6 +37,13 @@ def _mask(batch: int, length: int, pattern: str, gen: torch.Generator):
         mask[:, max(1, length // 4):] = False
     elif pattern == "all":
         mask[:] = False
+    elif pattern == "middle":
+        # kept keys only inside [L/3, 2L/3): the key loop skips tiles on both sides
+        mask[:, : length // 3] = False
+        mask[:, 2 * length // 3:] = False
+    elif pattern == "holes":
+        mask = torch.rand(batch, length, generator=gen) < 0.7
+        mask[:, 0] = True
     elif pattern == "boundary":
         choices = torch.tensor([1, 63, 64, 65, 127, 129, 383, 384, 511, 512])
         lens = choices[torch.arange(batch) % len(choices)].clamp(max=length)
@@ -123,7 +130,8 @@ def test_rel_kernel_boundary_lengths(length, dtype):
     _check(out, *args, True, True, f"L={length}")
 
 
-@pytest.mark.parametrize("pattern", ["none", "right", "left", "heavy", "all", "boundary"])
+@pytest.mark.parametrize("pattern", ["none", "right", "left", "heavy", "all", "boundary", "middle",
+                                     "holes"])
 @pytest.mark.parametrize("dtype", list(DTYPES))
 def test_rel_kernel_mask_patterns(pattern, dtype):
     args = _inputs(10, 2, 384, 64, DTYPES[dtype], pattern, seed=11)
