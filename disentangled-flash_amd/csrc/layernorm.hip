@@ -10,7 +10,9 @@
 //   s = T(x + r);  y = T((s - mean(s)) * rsqrt(var(s) + eps) * gamma + beta)
 //
 // HBM traffic per row: read x and r, write y (3 * H * sizeof(T) bytes), which
-// replaces the add's read-read-write plus the LayerNorm's read-write.
+// replaces the add's read-read-write plus the LayerNorm's read-write.  Rows
+// made of 16-byte chunks with 16-byte aligned pointers take the wide kernel
+// (16-byte accesses); others the 4-element one.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -93,6 +95,121 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
   }
 }
 
+// Wide variant: 16-byte loads, LANES lanes per row (32 or 64, so 8 or 4 rows
+// per 256-thread block), CH 16-byte chunks per lane.  Used when a row is a
+// whole number of 16-byte chunks and every pointer is 16-byte aligned; with
+// 32 lanes per row the reductions stay inside a half-wavefront.
+template <typename T>
+struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  typedef T type __attribute__((ext_vector_type(16 / sizeof(T))));
+};
+
+template <int LANES>
+__device__ inline float group_sum(float v) {
+#pragma unroll
+  for (int m = LANES / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+template <typename T, int LANES, int CH>
+__global__ __launch_bounds__(256) void add_layernorm_wide_kernel(
+    const T* __restrict__ x, const T* __restrict__ r, const T* __restrict__ gamma,
+    const T* __restrict__ beta, T* __restrict__ y, int rows, int hidden, float eps) {
+  using V = typename Vec16<T>::type;
+  constexpr int N = Vec16<T>::N;
+  const int sub = threadIdx.x % LANES;
+  const int row = blockIdx.x * (256 / LANES) + threadIdx.x / LANES;
+  if (row >= rows) return;  // whole lane groups exit together
+  const int64_t base = static_cast<int64_t>(row) * hidden;
+  const int nvec = hidden / N;
+
+  V a[CH];
+  V b[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int v = sub + LANES * k;
+    if (v < nvec) {
+      a[k] = *reinterpret_cast<const V*>(x + base + N * v);
+      b[k] = *reinterpret_cast<const V*>(r + base + N * v);
+    }
+  }
+  float s[CH][N];
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const bool live = sub + LANES * k < nvec;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      s[k][e] = live ? static_cast<float>(static_cast<T>(static_cast<float>(a[k][e]) +
+                                                         static_cast<float>(b[k][e])))
+                     : 0.0f;
+      sum += s[k][e];
+    }
+  }
+  const float inv_h = 1.0f / static_cast<float>(hidden);
+  const float mean = group_sum<LANES>(sum) * inv_h;
+  float sq = 0.0f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    if (sub + LANES * k < nvec) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float d = s[k][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float rstd = rsqrtf(group_sum<LANES>(sq) * inv_h + eps);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int v = sub + LANES * k;
+    if (v < nvec) {
+      const V g = *reinterpret_cast<const V*>(gamma + N * v);
+      const V bb = *reinterpret_cast<const V*>(beta + N * v);
+      V out;
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        out[e] = static_cast<T>((s[k][e] - mean) * rstd * static_cast<float>(g[e]) +
+                                static_cast<float>(bb[e]));
+      *reinterpret_cast<V*>(y + base + N * v) = out;
+    }
+  }
+}
+
+template <typename T, int LANES, int CH>
+int launch_ln_wide(const void* x, const void* r, const void* gamma, const void* beta, void* y,
+                   int rows, int hidden, float eps, hipStream_t stream) {
+  constexpr int kRows = 256 / LANES;
+  const int blocks = (rows + kRows - 1) / kRows;
+  hipLaunchKernelGGL((add_layernorm_wide_kernel<T, LANES, CH>), dim3(blocks), dim3(256), 0, stream,
+                     static_cast<const T*>(x), static_cast<const T*>(r),
+                     static_cast<const T*>(gamma), static_cast<const T*>(beta),
+                     static_cast<T*>(y), rows, hidden, eps);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Rows of up to 32 * 4 chunks use 32 lanes, longer rows 64 (<= 64 * 8 chunks,
+// i.e. hidden <= 4096 for 16-bit types and <= 2048 for fp32).  Returns
+// kWideUnfit when the shape does not fit the wide kernel.
+constexpr int kWideUnfit = -1000;
+
+template <typename T>
+int dispatch_ln_wide(const void* x, const void* r, const void* gamma, const void* beta, void* y,
+                     int rows, int hidden, float eps, hipStream_t stream) {
+  constexpr int N = Vec16<T>::N;
+  if (hidden % N != 0) return kWideUnfit;
+  const int nvec = hidden / N;
+  if (nvec <= 32) return launch_ln_wide<T, 32, 1>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  if (nvec <= 64) return launch_ln_wide<T, 32, 2>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  if (nvec <= 96) return launch_ln_wide<T, 32, 3>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  if (nvec <= 128) return launch_ln_wide<T, 32, 4>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  if (nvec <= 192) return launch_ln_wide<T, 64, 3>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  if (nvec <= 256) return launch_ln_wide<T, 64, 4>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  if (nvec <= 512) return launch_ln_wide<T, 64, 8>(x, r, gamma, beta, y, rows, hidden, eps, stream);
+  return kWideUnfit;
+}
+
 template <typename T, int VPL>
 int launch_ln(const void* x, const void* r, const void* gamma, const void* beta, void* y,
               int rows, int hidden, float eps, hipStream_t stream) {
@@ -138,6 +255,16 @@ extern "C" int dflash_add_layernorm_fwd(const void* x, const void* residual, con
                             reinterpret_cast<uintptr_t>(out);
   if (addr_or % (4 * esize) != 0) return DFLASH_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (addr_or % 16 == 0) {
+    int rc = kWideUnfit;
+    switch (dtype) {
+      case DFLASH_DTYPE_FP16: rc = dispatch_ln_wide<_Float16>(x, residual, gamma, beta, out, rows, hidden, eps, s); break;
+      case DFLASH_DTYPE_BF16: rc = dispatch_ln_wide<__bf16>(x, residual, gamma, beta, out, rows, hidden, eps, s); break;
+      case DFLASH_DTYPE_FP32: rc = dispatch_ln_wide<float>(x, residual, gamma, beta, out, rows, hidden, eps, s); break;
+      default: return DFLASH_ERR_DTYPE;
+    }
+    if (rc != kWideUnfit) return rc;
+  }
   switch (dtype) {
     case DFLASH_DTYPE_FP16: return dispatch_ln<_Float16>(x, residual, gamma, beta, out, rows, hidden, eps, s);
     case DFLASH_DTYPE_BF16: return dispatch_ln<__bf16>(x, residual, gamma, beta, out, rows, hidden, eps, s);
