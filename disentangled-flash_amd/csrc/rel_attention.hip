@@ -121,7 +121,7 @@ __device__ inline float add2(float s, T a, T b) {
 // same order, so P^T and V^T pair up in the PV product.
 __device__ constexpr int key_of(int x) { return (x & 3) * 4 + (x >> 2); }
 
-template <typename T, int D, int QW, int BN>
+template <typename T, int D, int QW, int BN, int VBUFS>
 struct RelLayout {
   static constexpr int BM = kWaves * QW;                // query rows per workgroup
   static constexpr int NCC = (QW + BN - 1 + 15) / 16;   // c2p window chunks per wavefront
@@ -141,18 +141,18 @@ struct RelLayout {
 
   static constexpr size_t ks_off = 0;
   static constexpr size_t vt_off = ks_off + size_t(BN) * KS_LD * sizeof(T);
-  static constexpr size_t pw_off = vt_off + 2 * size_t(VT_SIZE) * sizeof(T);
+  static constexpr size_t pw_off = vt_off + VBUFS * size_t(VT_SIZE) * sizeof(T);
   static constexpr size_t cw_off = pw_off + size_t(BN) * PW_LD * sizeof(T);
   static constexpr size_t bytes = cw_off + size_t(kWaves) * QW * CW_LD * sizeof(T);
 };
 
 }  // namespace
 
-template <typename T, int D, int QW, int BN, bool C2P, bool P2C>
-__global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p) {
+template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C>
+__global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
   using M = Mma<T>;
   using F = typename M::frag;
-  using LY = RelLayout<T, D, QW, BN>;
+  using LY = RelLayout<T, D, QW, BN, VBUFS>;
   constexpr int BM = LY::BM;
   constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
   constexpr int KB = BN / 16;           // 16-key blocks per tile
@@ -388,27 +388,36 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   u32x4_t pk[NCH];
   u32x2_t pv[NVB][4];
   uint8_t pmask = 0;
-  auto prefetch_kv = [&](int j0) {
+  auto prefetch_k = [&](int j0) {
     const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
 #pragma unroll
     for (int n = 0; n < NCH; ++n)
       if (NKC >= kThreads || tid < NKC) pk[n] = load16(rk, koff[n] + jb);
+    pmask = load1(rmask, static_cast<uint32_t>(j0 + lane));
+  };
+  auto prefetch_v = [&](int j0) {
+    const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
 #pragma unroll
     for (int n = 0; n < NVB; ++n)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
         if (NVBT >= kThreads || tid < NVBT) pv[n][rr] = load8(rv, voff[n] + jb + 4 * rr * sl_bytes);
-    pmask = load1(rmask, static_cast<uint32_t>(j0 + lane));
   };
 
   // ---- staging and window helpers ----
-  // V^T is double-buffered: tile n reads buffer n & 1 while tile n+1 is staged
-  // into the other one, so K/V of the next tile go to LDS right after the p2c
-  // barrier instead of behind a third barrier.
-  auto stage_kv = [&](T* vt) {
+  // K of tile n+1 is staged right after the p2c barrier of tile n (every
+  // wavefront has finished reading K of tile n).  V^T has two placements:
+  //   * two buffers: V of tile n+1 goes into the other buffer at the same
+  //     point, while tile n still reads its own;
+  //   * one buffer: V of tile n is staged after the first barrier of tile n
+  //     (every wavefront has finished PV of tile n-1) and read after the
+  //     second, which halves its LDS.
+  auto stage_k = [&]() {
 #pragma unroll
     for (int n = 0; n < NCH; ++n)
       if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
+  };
+  auto stage_v = [&](T* vt) {
 #pragma unroll
     for (int n = 0; n < NVB; ++n) {
       if (NVBT < kThreads && tid >= NVBT) break;
@@ -515,13 +524,16 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     }
     lutp = lut_load(lut_p_index(jstart + BN, 0));
   }
-  prefetch_kv(jstart);
-  stage_kv(Vt);
+  prefetch_k(jstart);
+  prefetch_v(jstart);
+  stage_k();
+  if constexpr (VBUFS == 2) stage_v(Vt);
   uint64_t kept_cur = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
   uint64_t kept_next = 0;
   c2p_products();
   c2p_store();
-  prefetch_kv(jstart + BN);
+  prefetch_k(jstart + BN);
+  if constexpr (VBUFS == 2) prefetch_v(jstart + BN);
   load_crow(jstart + BN);
 
   // ---- accumulators ----
@@ -553,6 +565,10 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
   for (int j0 = jstart; j0 < jend; j0 += BN) {
     const int jn = j0 + BN;
     lds_barrier();
+    if constexpr (VBUFS == 1) {
+      stage_v(Vt);
+      prefetch_v(jn);
+    }
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
     f32x4_t sc[KB][kQB];
@@ -599,10 +615,12 @@ __global__ __launch_bounds__(kThreads, 2) void rel_attention_kernel(RelParams p)
     // Next-tile work runs unconditionally (no branch splits the scheduling
     // region): past the last tile the buffer loads read zeros and the LDS
     // writes land in buffers nothing reads any more.
-    const T* vt_cur = Vt + vbuf * LY::VT_SIZE;
-    stage_kv(Vt + (vbuf ^ 1) * LY::VT_SIZE);
+    const T* vt_cur = Vt + (VBUFS == 2 ? vbuf * LY::VT_SIZE : 0);
+    stage_k();
+    if constexpr (VBUFS == 2) stage_v(Vt + (vbuf ^ 1) * LY::VT_SIZE);
     kept_next = __ballot(pmask != 0);
-    prefetch_kv(jn + BN);
+    prefetch_k(jn + BN);
+    if constexpr (VBUFS == 2) prefetch_v(jn + BN);
     c2p_products();
 
     // ---- relative scores ----
@@ -766,15 +784,29 @@ template <int D>
 constexpr int rel_block_n() {
   return 64;
 }
+// V^T buffers in LDS and workgroups per CU the registers are budgeted for.
+// d = 128 keeps one V^T buffer so that two workgroups fit in the LDS of a CU
+// (65 KB each instead of 82 KB): 153 -> 117 us at B=16, L=512, H=8, fp16.
+// For d <= 64 (two workgroups either way) both placements time the same.
+template <int D>
+constexpr int rel_v_buffers() {
+  return D >= 128 ? 1 : 2;
+}
+template <int D>
+constexpr int rel_workgroups_per_cu() {
+  return 2;
+}
 
 template <typename T, int D, bool C2P, bool P2C>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int QW = rel_queries_per_wave<D>();
   constexpr int BN = rel_block_n<D>();
-  using LY = RelLayout<T, D, QW, BN>;
+  constexpr int VB = rel_v_buffers<D>();
+  constexpr int WGS = rel_workgroups_per_cu<D>();
+  using LY = RelLayout<T, D, QW, BN, VB>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
-  auto kernel = rel_attention_kernel<T, D, QW, BN, C2P, P2C>;
+  auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C>;
   hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(LY::bytes));
