@@ -18,7 +18,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load torch's HIP runtime first)
 
 LIBRARY_NAME = "libdflash.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODES = {
     torch.float16: 0,
@@ -64,6 +64,14 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.dflash_add_layernorm_fwd.argtypes = [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, residual, gamma, beta, out
         _c_int, _c_int, _c_float, _c_int,                        # rows, hidden, eps, dtype
+        _c_void_p,                                               # stream
+    ]
+    lib.dflash_conv_layer_tail_fwd.restype = _c_int
+    lib.dflash_conv_layer_tail_fwd.argtypes = [
+        _c_void_p, _c_int,                                       # z, z_dtype
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,              # residual, bias, gamma, beta
+        _c_void_p, _c_void_p,                                    # mask, out
+        _c_int, _c_int, _c_int, _c_float, _c_int, _c_int,        # B, L, hidden, eps, act, dtype
         _c_void_p,                                               # stream
     ]
     lib.dflash_error_string.restype = ctypes.c_char_p

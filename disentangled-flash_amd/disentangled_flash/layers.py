@@ -7,8 +7,15 @@ epilogue) and replaces the separate residual add and LayerNorm with one
 kernel, ``disentangled_flash::add_layernorm``, which reads the projection and
 the residual once and writes the normalised row.
 
-The op has a fake implementation so that ``torch.compile(fullgraph=True)``
-traces through it, like the attention ops.
+The ``ConvLayer`` run after the first encoder layer (reference
+``_reference.py:519-566``, called at ``deberta.py:272-273``) is fused the same
+way: its Conv1d (kernel 3, padding 1) becomes one library GEMM of the layer
+input with the three taps side by side, and one kernel,
+``disentangled_flash::conv_layer_tail``, sums the taps of neighbouring rows and
+applies the mask, activation, residual add, LayerNorm and output mask.
+
+The ops have fake implementations so that ``torch.compile(fullgraph=True)``
+traces through them, like the attention ops.
 """
 
 from __future__ import annotations
@@ -90,4 +97,121 @@ def output_block(module: nn.Module, hidden_states: torch.Tensor,
     return add_layernorm(projected, residual, norm.weight, norm.bias, norm.eps)
 
 
-__all__ = ["add_layernorm", "fusable_output_block", "output_block"]
+# ConvLayer.conv_act values the fused tail implements (DFLASH_ACT_* codes);
+# "gelu" is the exact erf form of Hugging Face's ACT2FN["gelu"].
+CONV_ACTIVATIONS = {"gelu": 0, "tanh": 1, "relu": 2}
+
+
+@torch.library.custom_op("disentangled_flash::conv_layer_tail", mutates_args=())
+def conv_layer_tail(
+    taps: torch.Tensor, residual: torch.Tensor, conv_bias: torch.Tensor, weight: torch.Tensor,
+    bias: torch.Tensor, mask: torch.Tensor, eps: float, act: int
+) -> torch.Tensor:
+    """ConvLayer output from the tap products ``taps`` ``[B*L, 3*hidden]``.
+
+    ``residual`` is ``[B, L, hidden]``; ``mask`` the caller's ``[B, L]`` mask
+    as int64 (a bool mask as 0/1).
+    """
+
+    lib = _lib.load()
+    batch, length, hidden = residual.shape
+    out = torch.empty_like(residual)
+    code = lib.dflash_conv_layer_tail_fwd(
+        taps.data_ptr(),
+        _lib.DTYPE_CODES[taps.dtype],
+        residual.data_ptr(),
+        conv_bias.data_ptr(),
+        weight.data_ptr(),
+        bias.data_ptr(),
+        mask.data_ptr(),
+        out.data_ptr(),
+        batch,
+        length,
+        hidden,
+        float(eps),
+        int(act),
+        _lib.DTYPE_CODES[residual.dtype],
+        _lib.current_stream_handle(residual.device),
+    )
+    _lib.check(code, "dflash_conv_layer_tail_fwd")
+    return out
+
+
+@conv_layer_tail.register_fake
+def _conv_layer_tail_fake(taps, residual, conv_bias, weight, bias, mask, eps, act):
+    return torch.empty_like(residual)
+
+
+def fusable_conv_layer(module: nn.Module | None) -> bool:
+    """True for a Hugging Face ``ConvLayer`` the fused tail can run.
+
+    That is: ``conv`` an ``nn.Conv1d(hidden, hidden, 3, padding=1)`` with bias,
+    one group, unit stride and dilation and zero padding; ``conv_act`` one of
+    :data:`CONV_ACTIVATIONS`; an affine ``nn.LayerNorm`` over ``hidden``; a
+    ``dropout`` (the identity in inference); one dtype the kernel supports.
+    """
+
+    if module is None:
+        return False
+    conv = getattr(module, "conv", None)
+    norm = getattr(module, "LayerNorm", None)
+    if not isinstance(conv, nn.Conv1d) or conv.bias is None:
+        return False
+    if (conv.kernel_size != (3,) or conv.padding != (1,) or conv.stride != (1,)
+            or conv.dilation != (1,) or conv.groups != 1 or conv.padding_mode != "zeros"):
+        return False
+    hidden = conv.out_channels
+    if conv.in_channels != hidden or hidden % 4 != 0 or hidden > 4096:
+        return False
+    if getattr(module, "conv_act", None) not in CONV_ACTIVATIONS:
+        return False
+    if not isinstance(norm, nn.LayerNorm) or not norm.elementwise_affine or norm.bias is None:
+        return False
+    if tuple(norm.normalized_shape) != (hidden,):
+        return False
+    dtype = conv.weight.dtype
+    params = (conv.bias, norm.weight, norm.bias)
+    if dtype not in _lib.DTYPE_CODES or any(p.dtype != dtype for p in params):
+        return False
+    return hasattr(module, "dropout")
+
+
+def conv_taps(module: nn.Module) -> torch.Tensor:
+    """Conv1d weight ``[hidden, hidden, 3]`` as ``[3*hidden, hidden]``, tap-major."""
+
+    weight = module.conv.weight
+    hidden = weight.shape[0]
+    return weight.detach().permute(2, 0, 1).reshape(3 * hidden, hidden).contiguous()
+
+
+def conv_layer_block(module: nn.Module, taps: torch.Tensor, hidden_states: torch.Tensor,
+                     residual_states: torch.Tensor, input_mask: torch.Tensor) -> torch.Tensor:
+    """``module(hidden_states, residual_states, input_mask)`` for a 2-D mask.
+
+    The tap products are one GEMM with fp32 output for 16-bit inputs, so the
+    convolution is rounded once, in the tail kernel.
+    """
+
+    batch, length, hidden = hidden_states.shape
+    rows = hidden_states.reshape(batch * length, hidden)
+    if hidden_states.dtype == torch.float32:
+        products = torch.mm(rows, taps.t())
+    else:
+        products = torch.ops.aten.mm.dtype(rows, taps.t(), torch.float32)
+    mask = input_mask if input_mask.dtype == torch.int64 else input_mask.to(torch.int64)
+    residual = residual_states if residual_states.is_contiguous() else residual_states.contiguous()
+    norm = module.LayerNorm
+    return conv_layer_tail(products, residual, module.conv.bias, norm.weight, norm.bias,
+                           mask.contiguous(), norm.eps, CONV_ACTIVATIONS[module.conv_act])
+
+
+__all__ = [
+    "CONV_ACTIVATIONS",
+    "add_layernorm",
+    "conv_layer_block",
+    "conv_layer_tail",
+    "conv_taps",
+    "fusable_conv_layer",
+    "fusable_output_block",
+    "output_block",
+]

@@ -23,7 +23,7 @@ extern "C" {
 
 #define DFLASH_API __attribute__((visibility("default")))
 
-#define DFLASH_ABI_VERSION 2
+#define DFLASH_ABI_VERSION 3
 
 #define DFLASH_DTYPE_FP16 0
 #define DFLASH_DTYPE_BF16 1
@@ -36,6 +36,11 @@ extern "C" {
 #define DFLASH_ERR_DTYPE (-4)
 #define DFLASH_ERR_ALIGN (-5)
 #define DFLASH_ERR_TOO_LARGE (-6)
+
+/* Activation codes of the ConvLayer tail (the module's conv_act). */
+#define DFLASH_ACT_GELU 0 /* exact erf form, Hugging Face ACT2FN["gelu"] */
+#define DFLASH_ACT_TANH 1
+#define DFLASH_ACT_RELU 2
 
 /*
  * Fused attention over precomputed relative-score tables.
@@ -105,6 +110,31 @@ DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, cons
 DFLASH_API int dflash_add_layernorm_fwd(const void* x, const void* residual, const void* gamma,
                                         const void* beta, void* out, int rows, int hidden,
                                         float eps, int dtype, void* stream);
+
+/*
+ * Tail of the ConvLayer applied after the first encoder layer.
+ *
+ * Replaces ConvLayer.forward (/root/reference/src/disentangled_flash/_reference.py:536-566)
+ * as called by the encoder loop (/root/reference/src/disentangled_flash/deberta.py:272-273),
+ * from the convolution output on, for Conv1d(hidden, hidden, 3, padding=1, groups=1):
+ *   z          : [B*L, 3*hidden], dtype `z_dtype` (fp32, or `dtype`): the products of
+ *                the layer input rows with the three taps, z[:, k*hidden + o] =
+ *                sum_i x[:, i] * conv.weight[o, i, k]
+ *   residual   : [B*L, hidden], dtype `dtype` (the layer-0 output, residual_states)
+ *   conv_bias, gamma, beta : [hidden], dtype `dtype` (conv.bias, LayerNorm weight/bias)
+ *   mask       : int64 [B, L], the caller's attention mask (a bool mask passed as 0/1)
+ *   out        : [B*L, hidden], dtype `dtype`
+ *   act        : DFLASH_ACT_* (the module's conv_act)
+ * out = T(LayerNorm(T(residual + T(act(T(conv) or 0 where mask != 1)))) * T(mask)), conv
+ * summed in fp32 from the taps at l-1, l, l+1 of the same sequence plus conv_bias.
+ * hidden must be a multiple of 4 and at most 4096; pointers 4-element aligned, mask
+ * 8-byte aligned.  B*L == 0 is a no-op.
+ */
+DFLASH_API int dflash_conv_layer_tail_fwd(const void* z, int z_dtype, const void* residual,
+                                          const void* conv_bias, const void* gamma,
+                                          const void* beta, const int64_t* mask, void* out,
+                                          int B, int L, int hidden, float eps, int act, int dtype,
+                                          void* stream);
 
 /* Text for a return code of any dflash_* entry point. */
 DFLASH_API const char* dflash_error_string(int code);

@@ -94,3 +94,111 @@ def test_output_block_matches_huggingface_modules():
             expected = module(h, res)
             got = output_block(module, h, res)
         assert (got.float() - expected.float()).abs().max().item() <= 8e-3
+
+
+# ConvLayer tail (reference _reference.py:519-566).  Reference: the module's
+# steps in float64 from the exact convolution, rounding to the dtype wherever the
+# module produces a tensor (convolution output, activation, residual sum,
+# LayerNorm output, masked output).  The fused path rounds the fp32 sum of the
+# three taps, so it may differ from the exactly rounded convolution by an ulp at
+# a rounding boundary, which the later steps carry to about two output ulps:
+# |out - ref| <= REL * |ref| + ABS.  The Hugging Face module itself (MIOpen
+# convolution, bias added in the dtype) lands up to about three output ulps from
+# the float64 steps, so the fused output is held to three times the band from it.
+CONV_TOLS = {torch.float16: (2.0 ** -9, 2e-3), torch.bfloat16: (2.0 ** -6, 1.6e-2),
+             torch.float32: (1e-5, 5e-5)}
+
+
+def _conv_emulated(module, x, res, mask):
+    dt = x.dtype
+    conv = module.conv
+    full = F.conv1d(x.double().transpose(1, 2), conv.weight.double(), conv.bias.double(),
+                    padding=1).transpose(1, 2)
+    c = full.to(dt).double() * (mask == 1)[..., None]
+    act = {"gelu": F.gelu, "tanh": torch.tanh, "relu": torch.relu}[module.conv_act]
+    a = act(c).to(dt).double()
+    s = (res.double() + a).to(dt).double()
+    norm = module.LayerNorm
+    y = F.layer_norm(s, (s.shape[-1],), norm.weight.double(), norm.bias.double(), norm.eps)
+    return (y.to(dt).double() * mask.to(dt).double()[..., None]).to(dt)
+
+
+def _conv_module(hidden, act, dtype, seed):
+    from transformers import DebertaV2Config
+    from transformers.models.deberta_v2.modeling_deberta_v2 import ConvLayer
+
+    cfg = DebertaV2Config(hidden_size=hidden, conv_kernel_size=3, conv_act=act,
+                          hidden_dropout_prob=0.0, layer_norm_eps=1e-7)
+    torch.manual_seed(seed)
+    module = ConvLayer(cfg).eval()
+    with torch.no_grad():
+        module.conv.weight.normal_(0.0, 0.02)
+        module.conv.bias.normal_(0.0, 0.05)
+        module.LayerNorm.weight.normal_(1.0, 0.1)
+        module.LayerNorm.bias.normal_(0.0, 0.1)
+    return module.to("cuda", dtype)
+
+
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("act", ["gelu", "tanh", "relu"])
+@pytest.mark.parametrize("batch,length,hidden", [(3, 37, 768), (2, 1, 64), (2, 130, 1536)])
+def test_conv_layer_block_matches_huggingface(dtype, act, batch, length, hidden):
+    from disentangled_flash.layers import conv_layer_block, conv_taps, fusable_conv_layer
+
+    dt = DTYPES[dtype]
+    module = _conv_module(hidden, act, dt, seed=batch * 100 + length)
+    assert fusable_conv_layer(module)
+    gen = torch.Generator().manual_seed(length)
+    x = (torch.randn(batch, length, hidden, generator=gen) * 0.5).to("cuda", dt)
+    res = torch.randn(batch, length, hidden, generator=gen).to("cuda", dt)
+    lengths = torch.randint(1, length + 1, (batch,), generator=gen)
+    mask = (torch.arange(length)[None] < lengths[:, None]).long().cuda()
+    with torch.inference_mode():
+        expected = module(x, res, mask)
+        got = conv_layer_block(module, conv_taps(module), x, res, mask)
+        got_bool = conv_layer_block(module, conv_taps(module), x, res, mask.bool())
+    torch.cuda.synchronize()
+    ref = _conv_emulated(module, x, res, mask).double()
+    rel, abs_tol = CONV_TOLS[dt]
+    bound = rel * ref.abs() + abs_tol
+    err = (got.double() - ref).abs()
+    assert torch.isfinite(got).all()
+    assert bool((err <= bound).all()), f"max err vs float64 steps {err.max().item():.3e}"
+    module_err = (got.double() - expected.double()).abs()
+    assert bool((module_err <= 3 * bound).all()), f"max err vs module {module_err.max().item():.3e}"
+    assert torch.equal(got, got_bool)  # a bool mask means the same as its 0/1 form
+    # padded positions are exactly zero, as output * mask makes them
+    assert bool((got[mask == 0] == 0).all())
+
+
+def test_conv_layer_block_numeric_mask_values():
+    """A numeric mask keeps the convolution only where it equals 1 and scales by it."""
+
+    from disentangled_flash.layers import conv_layer_block, conv_taps
+
+    module = _conv_module(256, "tanh", torch.float32, seed=5)
+    x = torch.randn(2, 9, 256, device="cuda")
+    res = torch.randn(2, 9, 256, device="cuda")
+    mask = torch.tensor([[1, 1, 2, 0, 1, 1, 1, 0, 0], [1] * 9], device="cuda")
+    with torch.inference_mode():
+        expected = module(x, res, mask)
+        got = conv_layer_block(module, conv_taps(module), x, res, mask)
+    assert (got - expected).abs().max().item() <= 5e-5
+
+
+def test_conv_layer_tail_rejects_bad_arguments():
+    from disentangled_flash import _lib
+
+    lib = _lib.load()
+    y = torch.zeros(64, device="cuda")
+    m = torch.ones(4, dtype=torch.int64, device="cuda")
+
+    def call(z_dtype=2, batch=1, hidden=8, act=0):
+        return lib.dflash_conv_layer_tail_fwd(y.data_ptr(), z_dtype, y.data_ptr(), y.data_ptr(),
+                                              y.data_ptr(), y.data_ptr(), m.data_ptr(),
+                                              y.data_ptr(), batch, 4, hidden, 1e-5, act, 2, None)
+
+    assert call(act=7) == -2        # unknown activation
+    assert call(hidden=6) == -2     # hidden not a multiple of 4
+    assert call(z_dtype=1) == -4    # taps neither fp32 nor the dtype
+    assert call(batch=0) == 0       # empty batch is a no-op

@@ -279,3 +279,43 @@ def test_fusable_output_block_rules():
     other.LayerNorm = nn.LayerNorm(64, elementwise_affine=False)
     assert not fusable_output_block(other)
     assert not fusable_output_block(nn.Linear(4, 4))
+
+
+def test_fusable_conv_layer_rules_and_tap_decomposition():
+    """The fused ConvLayer path's eligibility, and the tap split it relies on.
+
+    The convolution output at position l is z_0[l-1] + z_1[l] + z_2[l+1] + bias
+    with z = x . conv_taps(module)^T, the out-of-range taps dropped; checked
+    against torch's own Conv1d on the CPU.
+    """
+
+    from torch.nn import functional as F
+    from transformers import DebertaV2Config
+    from transformers.models.deberta_v2.modeling_deberta_v2 import ConvLayer
+
+    from disentangled_flash.layers import conv_taps, fusable_conv_layer
+
+    def make(**kw):
+        cfg = DebertaV2Config(hidden_size=32, conv_kernel_size=kw.get("k", 3),
+                              conv_act=kw.get("act", "gelu"), conv_groups=kw.get("groups", 1),
+                              hidden_dropout_prob=0.0)
+        return ConvLayer(cfg).eval()
+
+    assert fusable_conv_layer(make())
+    assert fusable_conv_layer(make(act="tanh")) and fusable_conv_layer(make(act="relu"))
+    assert not fusable_conv_layer(make(act="sigmoid"))
+    assert not fusable_conv_layer(make(k=5))
+    assert not fusable_conv_layer(make(groups=2))
+    assert not fusable_conv_layer(None)
+
+    module = make()
+    gen = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 7, 32, generator=gen, dtype=torch.float64)
+    conv = module.conv.double()
+    expected = F.conv1d(x.transpose(1, 2), conv.weight, conv.bias, padding=1).transpose(1, 2)
+    z = x.reshape(14, 32) @ conv_taps(module).double().t()
+    z = z.reshape(2, 7, 3, 32)
+    got = z[:, :, 1] + conv.bias
+    got[:, 1:] += z[:, :-1, 0]
+    got[:, :-1] += z[:, 1:, 2]
+    assert torch.allclose(got, expected, atol=1e-12)
