@@ -247,6 +247,59 @@ def bench_encoder(batch: int, length: int, steps: int, warmup: int,
     return results
 
 
+def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
+                lengths=(16, 32, 64, 128, 256, 384, 512)):
+    """C3 sweep: 12-layer fp16 encoder latency over B x L for original / optimized / hip.
+
+    ``hip_graph_ms`` replays the hip encoder from a HIP graph captured for that (B, L).
+
+    One random-init model; the ``optimized`` and ``hip`` copies are prepared for every
+    bucket once, then each (B, L) is timed with the bucket activated (median of
+    individually event-timed forwards, launch gaps included).
+    """
+
+    import copy
+
+    from transformers import DebertaV2Model
+
+    from disentangled_flash import enable_deberta_inference
+
+    torch.manual_seed(17)
+    base = DebertaV2Model(encoder_config()).to("cuda", torch.float16).eval()
+    from disentangled_flash import capture_deberta_buckets
+
+    prepared = {}
+    for backend in ("optimized", "hip"):
+        model = copy.deepcopy(base)
+        enable_deberta_inference(model, backend=backend, sequence_lengths=list(lengths))
+        prepared[backend] = model.encoder
+    rows = []
+    with torch.inference_mode():
+        for length in lengths:
+            for batch in batches:
+                hidden, mask = encoder_inputs(batch, length, torch.float16, "cuda")
+                row = {"batch": batch, "seq_len": length}
+                row["original_ms"] = time_p50(
+                    lambda: base.encoder(hidden, mask, output_hidden_states=False), steps, warmup)
+                for backend, encoder in prepared.items():
+                    encoder.activate_shape(length)
+                    plans = encoder._active_plans
+                    row[f"{backend}_ms"] = time_p50(
+                        lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: B023
+                                                         output_hidden_states=False),
+                        steps, warmup)
+                # the hip encoder replayed from a HIP graph (input copies included)
+                bucket = capture_deberta_buckets(prepared["hip"], [(batch, length)])[
+                    (batch, length)]
+                row["hip_graph_ms"] = time_p50(lambda: bucket(hidden, mask),  # noqa: B023
+                                               steps, warmup)
+                del bucket
+                row = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
+                log(json.dumps(row))
+                rows.append(row)
+    return rows
+
+
 def cpu_baseline(target_seconds: float = 12.0):
     """Oracle restatement of the ``optimized`` equation, fp32, on the host CPU.
 
@@ -300,6 +353,8 @@ def main() -> int:
                         help="launch only the fused C2 kernel --steps times (profiling driver)")
     parser.add_argument("--encoder-only", action="store_true",
                         help="time only the hip 12-layer encoder (profiling driver)")
+    parser.add_argument("--sweep", action="store_true",
+                        help="C3 encoder sweep B x L (original / optimized / hip), one JSON line")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="one 256 MiB device-to-device copy (HBM counter calibration)")
     args = parser.parse_args()
@@ -325,6 +380,11 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copied {src.numel() * src.element_size()} bytes")
+        return 0
+    if args.sweep:
+        rows = bench_sweep(max(5, args.encoder_steps // 2), 3)
+        print(json.dumps({"sweep": "C3 12-layer encoder fp16, ms (median)", "rows": rows}),
+              flush=True)
         return 0
     if args.encoder_only:
         enc = bench_encoder(32, 512, args.encoder_steps, 3, backends=("hip",))

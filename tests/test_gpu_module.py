@@ -244,3 +244,40 @@ def test_optimize_deberta_on_full_model_and_compile():
     assert ((got.float() - expected.float()).abs() * valid).max().item() <= 2e-2
     # Inductor re-fuses the fp16 LayerNorm/GELU epilogues; outputs are O(1) in fp16.
     assert (traced.float() - eager.float()).abs().max().item() <= 1e-2
+
+
+def test_hip_graph_buckets_replay_eager_results():
+    """Captured encoder buckets reproduce the eager forward on every replay.
+
+    Several replays per bucket with new inputs, interleaved with eager work and
+    host synchronisation, each checked against the eager forward of the same
+    inputs (same kernels, same launch order: identical results expected).
+    """
+
+    from disentangled_flash import capture_deberta_buckets, enable_deberta_inference
+
+    base = _encoder_model(2, 768, 12, 3072)
+    model = enable_deberta_inference(base.to("cuda", torch.float16), backend="hip",
+                                     sequence_lengths=[64, 128, 512])
+    encoder = model.encoder
+    # (32, 512) is the C3 shape, where hipBLASLt picks its stream-K kernels
+    buckets = capture_deberta_buckets(encoder, [(2, 64), (3, 128), (2, 64), (32, 512)])
+    assert sorted(buckets) == [(2, 64), (3, 128), (32, 512)]
+    with torch.inference_mode():
+        for replay in range(3):
+            for (batch, length), bucket in buckets.items():
+                hidden, mask = _encoder_inputs(batch, length, 768, seed=100 + replay + length)
+                hidden, mask = hidden.to("cuda", torch.float16), mask.cuda()
+                plans = encoder._prepared_plans[length]
+                eager = encoder.forward_prepared(hidden, mask, plans,
+                                                 output_hidden_states=False).last_hidden_state
+                torch.cuda.synchronize()
+                got = bucket(hidden, mask).clone()
+                torch.cuda.synchronize()
+                diff = (got.float() - eager.float()).abs().max().item()
+                assert diff == 0.0, f"replay {replay} bucket {(batch, length)}: {diff:.3e}"
+        with pytest.raises(ValueError, match="bucket expects"):
+            buckets[(2, 64)](torch.zeros(1, 64, 768, device="cuda", dtype=torch.float16),
+                             torch.ones(1, 64, device="cuda", dtype=torch.long))
+    with pytest.raises(ValueError, match="not a prepared bucket"):
+        capture_deberta_buckets(encoder, [(1, 32)])
