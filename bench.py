@@ -43,7 +43,8 @@ def log(message: str) -> None:
 
 
 def c2_inputs(dtype: torch.dtype, padded: bool, seed: int = 2024, batch: int = 32,
-              heads: int = 12, length: int = 512, dim: int = 64, device: str = "cuda"):
+              heads: int = 12, length: int = 512, dim: int = 64, device: str = "cuda",
+              valid_lengths=None):
     """Q/K/V and Qr/Kr ~ N(0,1)/sqrt(d); lengths U[256, 512] or none."""
 
     from disentangled_flash.position import compact_position_plan
@@ -55,7 +56,11 @@ def c2_inputs(dtype: torch.dtype, padded: bool, seed: int = 2024, batch: int = 3
     q, k, v = (torch.randn(batch, heads, length, dim, generator=gen) * scale for _ in range(3))
     pos_key, pos_query = (torch.randn(heads, active.numel(), dim, generator=gen) * scale
                           for _ in range(2))
-    if padded:
+    if valid_lengths is not None:
+        choices = torch.tensor(list(valid_lengths))
+        lengths = choices[torch.arange(batch) % len(choices)].clamp(max=length)
+        mask = torch.arange(length)[None] < lengths[:, None]
+    elif padded:
         lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen)
         mask = torch.arange(length)[None] < lengths[:, None]
     else:
@@ -106,13 +111,13 @@ def time_p50(fn, steps: int, warmup: int) -> float:
     return statistics.median(samples)
 
 
-def fused_call(inp):
+def fused_call(inp, has_c2p: bool = True, has_p2c: bool = True):
     from disentangled_flash.kernel import deberta_attention_rel
 
-    scale_log2 = LOG2E / math.sqrt(3 * inp["dim"])
+    scale_log2 = LOG2E / math.sqrt((1 + int(has_c2p) + int(has_p2c)) * inp["dim"])
     return lambda: deberta_attention_rel(inp["qkv"], inp["pos_key"], inp["pos_query"], inp["lut"],
                                          inp["mask"], inp["heads"], inp["dim"], scale_log2,
-                                         True, True, True)
+                                         has_c2p, has_p2c, True)
 
 
 def table_call(inp):
@@ -300,6 +305,94 @@ def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
     return rows
 
 
+def bench_edge(steps: int, warmup: int):
+    """C5 edge sweep: the fused attention op for d=128/H=8 (B=16, L=512) and d=32/H=16
+    (B=16, L=384) in fp16/bf16/fp32 x {c2p, p2c, c2p|p2c}, boundary valid lengths
+    {1, 63, 64, 65, 127, 129, 383, 384, 511, 512} mixed in the batch."""
+
+    boundary = (1, 63, 64, 65, 127, 129, 383, 384, 511, 512)
+    rows = []
+    for dim, heads, length in ((128, 8, 512), (32, 16, 384)):
+        for name, dtype in DTYPES.items():
+            inp = c2_inputs(dtype, padded=True, batch=16, heads=heads, length=length, dim=dim,
+                            valid_lengths=boundary)
+            for mode, (c2p, p2c) in (("c2p", (True, False)), ("p2c", (False, True)),
+                                     ("c2p|p2c", (True, True))):
+                ms = time_launches(fused_call(inp, c2p, p2c), steps, warmup)
+                row = {"head_dim": dim, "heads": heads, "batch": 16, "seq_len": length,
+                       "dtype": name, "mode": mode, "us": round(ms * 1e3, 1),
+                       "tflops_f_attn": round(attention_flops(inp) / ms / 1e9, 1)}
+                log(json.dumps(row))
+                rows.append(row)
+            del inp
+            torch.cuda.empty_cache()
+    return rows
+
+
+def bench_c4(steps: int, warmup: int):
+    """C4: 24-layer DeBERTa-v2-xlarge-shaped encoder, bf16, B=8, one batch per bucket.
+
+    Valid lengths are log-normal (median 60) clipped to [16, 256]; each batch holds the
+    lengths that fall in its bucket {64, 128, 256}, padded to the bucket.
+    """
+
+    import copy
+
+    from transformers import DebertaV2Config, DebertaV2Model
+
+    from disentangled_flash import capture_deberta_buckets, enable_deberta_inference
+
+    config = DebertaV2Config(
+        vocab_size=128100, hidden_size=1536, num_hidden_layers=24, num_attention_heads=24,
+        intermediate_size=6144, hidden_act="gelu", hidden_dropout_prob=0.0,
+        attention_probs_dropout_prob=0.0, max_position_embeddings=512, type_vocab_size=0,
+        initializer_range=0.02, layer_norm_eps=1e-7, relative_attention=True,
+        max_relative_positions=512, position_buckets=256, pos_att_type=["p2c", "c2p"],
+        norm_rel_ebd="layer_norm", share_att_key=True, conv_kernel_size=3, conv_act="gelu",
+        position_biased_input=False,
+    )
+    torch.manual_seed(17)
+    base = DebertaV2Model(config).to("cuda", torch.bfloat16).eval()
+    buckets = (64, 128, 256)
+    prepared = {}
+    for backend in ("optimized", "hip"):
+        model = copy.deepcopy(base)
+        enable_deberta_inference(model, backend=backend, sequence_lengths=list(buckets))
+        prepared[backend] = model.encoder
+    gen = torch.Generator().manual_seed(23)
+    pool = torch.exp(torch.randn(4096, generator=gen) * 0.75 + math.log(60.0)).clamp(16, 256)
+    pool = pool.long()
+    rows = []
+    with torch.inference_mode():
+        lower = 0
+        for bucket in buckets:
+            in_bucket = (pool > lower) & (pool <= bucket)
+            lengths = pool[in_bucket][:8]
+            share = float(in_bucket.float().mean())
+            lower = bucket
+            mask = (torch.arange(bucket)[None] < lengths[:, None]).long().cuda()
+            hidden = (torch.randn(8, bucket, 1536, generator=gen) * 0.5).to("cuda", torch.bfloat16)
+            hidden = hidden * mask[..., None]
+            row = {"bucket": bucket, "batch": 8, "bucket_share": round(share, 3),
+                   "mean_valid": round(float(lengths.float().mean()), 1)}
+            row["original_ms"] = time_p50(
+                lambda: base.encoder(hidden, mask, output_hidden_states=False), steps, warmup)
+            for backend, encoder in prepared.items():
+                encoder.activate_shape(bucket)
+                plans = encoder._active_plans
+                row[f"{backend}_ms"] = time_p50(
+                    lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: B023
+                                                     output_hidden_states=False),
+                    steps, warmup)
+            graph = capture_deberta_buckets(prepared["hip"], [(8, bucket)])[(8, bucket)]
+            row["hip_graph_ms"] = time_p50(lambda: graph(hidden, mask), steps, warmup)  # noqa: B023
+            del graph
+            row = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in row.items()}
+            log(json.dumps(row))
+            rows.append(row)
+    return rows
+
+
 def cpu_baseline(target_seconds: float = 12.0):
     """Oracle restatement of the ``optimized`` equation, fp32, on the host CPU.
 
@@ -355,6 +448,10 @@ def main() -> int:
                         help="time only the hip 12-layer encoder (profiling driver)")
     parser.add_argument("--sweep", action="store_true",
                         help="C3 encoder sweep B x L (original / optimized / hip), one JSON line")
+    parser.add_argument("--edge", action="store_true",
+                        help="C5 head-dim / precision / mode sweep of the fused op, one JSON line")
+    parser.add_argument("--c4", action="store_true",
+                        help="C4 24-layer xlarge bf16 encoder per bucket, one JSON line")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="one 256 MiB device-to-device copy (HBM counter calibration)")
     args = parser.parse_args()
@@ -380,6 +477,15 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copied {src.numel() * src.element_size()} bytes")
+        return 0
+    if args.edge:
+        print(json.dumps({"edge": "C5 fused attention", "rows": bench_edge(args.steps, args.warmup)}),
+              flush=True)
+        return 0
+    if args.c4:
+        rows = bench_c4(max(5, args.encoder_steps // 2), 3)
+        print(json.dumps({"c4": "24-layer xlarge bf16 encoder, ms (median)", "rows": rows}),
+              flush=True)
         return 0
     if args.sweep:
         rows = bench_sweep(max(5, args.encoder_steps // 2), 3)
