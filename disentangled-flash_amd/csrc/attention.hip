@@ -618,11 +618,16 @@ int dispatch(const Params& prm, int D, int dtype, int has_c2p, int has_p2c, hipS
   return DFLASH_ERR_HEAD_DIM;
 }
 
+// Returned by check_common for an empty batch: the entry points report success
+// without launching (the reference's launch over an empty grid is a no-op too).
+constexpr int kEmptyBatch = 1;
+
 int check_common(const void* q, const void* k, const void* v, const int32_t* lut,
                  const uint8_t* mask, const void* out, int B, int H, int L, int D, int S,
                  int has_c2p, int has_p2c, int dtype) {
+  if (B < 0 || H < 1 || L < 1) return DFLASH_ERR_SHAPE;
+  if (B == 0) return kEmptyBatch;  // nothing to launch; empty tensors may carry null pointers
   if (!q || !k || !v || !mask || !out) return DFLASH_ERR_NULL;
-  if (B < 1 || H < 1 || L < 1) return DFLASH_ERR_SHAPE;
   if (D != 32 && D != 64 && D != 128) return DFLASH_ERR_HEAD_DIM;
   if (dtype < DFLASH_DTYPE_FP16 || dtype > DFLASH_DTYPE_FP32) return DFLASH_ERR_DTYPE;
   if (static_cast<int64_t>(L) * D >= (int64_t{1} << 31) ||
@@ -649,6 +654,7 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
   (void)strict_fp32;  // fp32 always runs IEEE fp32 MFMA on gfx950
   int rc = check_common(query, key, value, delta_to_local, attention_mask, out, B, H, L, D, S,
                         has_c2p, has_p2c, dtype);
+  if (rc == kEmptyBatch) return DFLASH_OK;
   if (rc != DFLASH_OK) return rc;
   if ((has_c2p && !c2p) || (has_p2c && !p2c)) return DFLASH_ERR_NULL;
   Params prm{};
@@ -681,6 +687,7 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
   (void)strict_fp32;
   int rc = check_common(query, key, value, delta_to_local, attention_mask, out, B, H, L, D, S,
                         has_c2p, has_p2c, dtype);
+  if (rc == kEmptyBatch) return DFLASH_OK;
   if (rc != DFLASH_OK) return rc;
   if ((has_c2p && !pos_key) || (has_p2c && !pos_query)) return DFLASH_ERR_NULL;
   const int esize = dtype == DFLASH_DTYPE_FP32 ? 4 : 2;

@@ -195,10 +195,11 @@ class HipPreparedPositionPlan(NamedTuple):
 
 
 def lut_is_window_safe(delta_to_local: torch.Tensor) -> bool:
-    """True if the LUT steps by 0 or 1 per delta, the fused kernel's precondition.
+    """True if the LUT steps by 0 or 1 per delta, the fused fp32 kernel's precondition.
 
-    Every plan built from a monotone bucket function satisfies it; a plan that
-    does not is run through the table path instead.
+    Every plan built from a monotone bucket function satisfies it.  The fp16/bf16
+    kernel computes relative scores per delta and accepts any LUT; an fp32 call
+    with a plan that fails this check runs through the table path instead.
     """
 
     if delta_to_local.numel() < 2:
@@ -312,7 +313,7 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
         fused = F.linear(hidden_states, self._cached_qkv_weight, self._cached_qkv_bias)
         if fused.stride(-1) != 1 or fused.stride(1) != fused.size(-1):
             fused = fused.contiguous()
-        if self.relative_mode == "fused" and plan.windowed:
+        if self.relative_mode == "fused" and (plan.windowed or fused.dtype != torch.float32):
             placeholder = plan.delta_to_local
             output = deberta_attention_rel(
                 fused,

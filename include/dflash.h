@@ -57,6 +57,8 @@ extern "C" {
  *   score_scale_log2  : log2(e) / sqrt(D * (1 + has_c2p + has_p2c))  (kernel.py:587-588)
  *   strict_fp32       : accepted for signature parity; gfx950 has no TF32 MFMA,
  *                       so fp32 always runs IEEE fp32 MFMA.
+ * B == 0 is a no-op that returns 0 (pointers are not inspected), like the
+ * reference's launch over an empty grid.
  */
 DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const void* value,
                          const void* c2p, const void* p2c, const int32_t* delta_to_local,
@@ -79,10 +81,13 @@ DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const vo
  *                       stride_h = D, stride_l = 3*H*D) - no head reshape copy.
  *   pos_key, pos_query: [H, S, D] contiguous, the plan's pos_key / pos_query
  *                       (kernel.py:461-468, 522-523)
- *   delta_to_local    : as above, and additionally non-decreasing with steps of
- *                       0 or 1 (true for every plan built from a monotone bucket
- *                       function; see position.py:89-128).  The kernel relies on
- *                       it to map a tile's deltas to a contiguous slot window.
+ *   delta_to_local    : as above.  For dtype fp32 it must additionally be
+ *                       non-decreasing with steps of 0 or 1 (true for every plan
+ *                       built from a monotone bucket function; see
+ *                       position.py:89-128): the fp32 kernel maps a tile's deltas
+ *                       to a contiguous slot window.  The fp16/bf16 kernel works
+ *                       per delta and accepts any table.
+ * B == 0 is a no-op that returns 0 (pointers are not inspected).
  */
 DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,
                              int64_t stride_b, int64_t stride_h, int64_t stride_l,

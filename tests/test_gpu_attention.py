@@ -214,3 +214,35 @@ def test_c_abi_rejects_bad_arguments():
                                   1, 0, 0, 1, None)
     assert rc == -1
     assert b"head dimension" in lib.dflash_error_string(-3)
+
+
+def test_empty_batch_is_a_no_op():
+    """B == 0 launches nothing and returns an empty output (an empty grid in the reference)."""
+
+    from disentangled_flash import _lib
+    from disentangled_flash.kernel import deberta_attention_rel
+
+    s, lut = _lut(64, "cuda")
+    qkv = torch.empty(0, 64, 3 * 2 * 64, device="cuda", dtype=torch.float16)
+    pos = torch.randn(2, s, 64, device="cuda", dtype=torch.float16)
+    mask = torch.empty(0, 64, device="cuda", dtype=torch.bool)
+    out = deberta_attention_rel(qkv, pos, pos, lut, mask, 2, 64, LOG2E / math.sqrt(192),
+                                True, True, True)
+    assert out.shape == (0, 64, 128)
+    lib = _lib.load()
+    assert lib.dflash_attention_fwd(None, None, None, None, None, None, None, None, 0, 2, 64, 64,
+                                    s, 1.0, 1, 1, 0, 1, None) == 0
+    assert lib.dflash_attention_fwd(None, None, None, None, None, None, None, None, -1, 2, 64, 64,
+                                    s, 1.0, 1, 1, 0, 1, None) == -2
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_rel_kernel_accepts_any_lut(dtype):
+    """The 16-bit kernel works per delta: a random (non-monotone) slot table is fine."""
+
+    args = list(_inputs(3, 2, 200, 64, DTYPES[dtype], "right", seed=21))
+    slots = args[3].shape[1]
+    gen = torch.Generator().manual_seed(4)
+    args[5] = torch.randint(0, slots, (2 * 200 - 1,), generator=gen, dtype=torch.int32).cuda()
+    out = _run_rel(*args, True, True)
+    _check(out, *args, True, True, "random lut")
