@@ -33,7 +33,6 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-#include <stdlib.h>
 
 #include "dflash.h"
 
@@ -701,7 +700,7 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
                             reinterpret_cast<uintptr_t>(pos_key) |
                             reinterpret_cast<uintptr_t>(pos_query);
   if (addr_or % 16 != 0) return DFLASH_ERR_ALIGN;
-  if (dtype != DFLASH_DTYPE_FP32 && !getenv("DFLASH_REL_V1")) {
+  if (dtype != DFLASH_DTYPE_FP32) {  // fp16 / bf16: per-delta relative windows
     RelParams rp{};
     rp.q = query;
     rp.k = key;
