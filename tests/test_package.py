@@ -319,3 +319,15 @@ def test_fusable_conv_layer_rules_and_tap_decomposition():
     got[:, 1:] += z[:, :-1, 0]
     got[:, :-1] += z[:, 1:, 2]
     assert torch.allclose(got, expected, atol=1e-12)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """The benchmark measures the single-GPU path; --gpus N > 1 exits with a message."""
+
+    import subprocess
+    import sys
+
+    result = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"],
+                            capture_output=True, text=True, timeout=300)
+    assert result.returncode == 2
+    assert "single-GPU" in result.stderr
