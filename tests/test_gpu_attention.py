@@ -246,3 +246,13 @@ def test_rel_kernel_accepts_any_lut(dtype):
     args[5] = torch.randint(0, slots, (2 * 200 - 1,), generator=gen, dtype=torch.int32).cuda()
     out = _run_rel(*args, True, True)
     _check(out, *args, True, True, "random lut")
+
+
+@pytest.mark.parametrize("length", [2048, 4096])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_rel_kernel_long_sequences(length, dtype):
+    """Sequences far past the bucketed range (every delta beyond +-256 shares the end slots)."""
+
+    args = _inputs(1, 2, length, 64, DTYPES[dtype], "right", seed=length + 1)
+    out = _run_rel(*args, True, True)
+    _check(out, *args, True, True, f"L={length}")
