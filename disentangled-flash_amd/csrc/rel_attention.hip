@@ -577,9 +577,10 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
     f32x4_t sc[KB][kQB];
-    // One straight-line copy per wavefront index, so that the chunks a
-    // wavefront skips are known at compile time and the MFMAs of the whole
-    // phase form one scheduling region.
+    // For d <= 64 one straight-line copy per wavefront index, so that the
+    // chunks a wavefront skips are known at compile time and the MFMAs of the
+    // whole phase form one scheduling region.  d = 128 keeps one copy with
+    // runtime skips (below): with four copies it runs out of registers.
     auto qk_p2c = [&](auto wave_c) {
       constexpr int W = decltype(wave_c)::value;
 #pragma unroll
@@ -610,11 +611,39 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
       }
     };
-    switch (wave) {
-      case 0: qk_p2c(IntC<0>{}); break;
-      case 1: qk_p2c(IntC<1>{}); break;
-      case 2: qk_p2c(IntC<2>{}); break;
-      default: qk_p2c(IntC<3>{}); break;
+    if constexpr (D <= 64) {
+      switch (wave) {
+        case 0: qk_p2c(IntC<0>{}); break;
+        case 1: qk_p2c(IntC<1>{}); break;
+        case 2: qk_p2c(IntC<2>{}); break;
+        default: qk_p2c(IntC<3>{}); break;
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        F kf[KD];
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd)
+          kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+#pragma unroll
+        for (int qb = 0; qb < kQB; ++qb) {
+          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd) acc = M::run(kf[kd], qf[qb][kd], acc);
+          sc[kb][qb] = acc;
+        }
+        if constexpr (P2C) {
+#pragma unroll
+          for (int u = 0; u < PU; ++u) {
+            const int pc = wave + kWaves * u;
+            if (pc < KB - 1 - kb || pc > (BM + BN - 2) / 16 - kb) continue;
+            f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kd = 0; kd < KD; ++kd) acc = M::run(prow[u][kd], kf[kd], acc);
+            store4<T>(Pw + (16 * kb + key_of(c)) * LY::PW_LD + 16 * pc + 4 * g, acc);
+          }
+        }
+      }
     }
     if constexpr (P2C) {
       // Next tile's p2c rows: shift the kept chunks up by 4, load the new one.
