@@ -58,6 +58,8 @@ namespace {
 
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef short s4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4_t lds_s4_t;
 
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, gfx9 family descriptor word 3
 
@@ -117,8 +119,9 @@ __device__ inline float add2(float s, T a, T b) {
 
 // Key of MFMA row x within a 16-key block: x = 4a + b holds key a + 4b, so
 // lane (c, g) of a 16x16 score block holds keys g + 4r (r = 0..3) and one
-// gather instruction (fixed r) touches four adjacent keys.  V^T columns use the
-// same order, so P^T and V^T pair up in the PV product.
+// gather instruction (fixed r) touches four adjacent keys.  The transposing
+// reads of the V operand use the same order, so P^T and V^T pair up in the PV
+// product.
 __device__ constexpr int key_of(int x) { return (x & 3) * 4 + (x >> 2); }
 
 template <int N>
@@ -133,7 +136,10 @@ struct RelLayout {
   static constexpr int NPC = (BM + BN - 1 + 15) / 16;   // p2c window chunks per workgroup
   static constexpr int PU = (NPC + kWaves - 1) / kWaves;  // p2c chunks per wavefront
   static constexpr int KS_LD = D + 8;                   // Ks[BN][KS_LD]
-  static constexpr int VT_LD = BN + 4;                  // Vt[D][VT_LD]
+  // V tile row-major, Vs[BN][VS_LD]: the row pad of 4 elements makes the
+  // transposing reads of the PV operand conflict-free (two passes per
+  // half-wavefront) with the staging stores at their minimum.
+  static constexpr int VS_LD = D + 4;
   // Row strides (in elements) chosen for the LDS of gfx950 as measured: 32
   // four-byte banks served per half-wavefront, a 2-byte read of two lanes in
   // one dword is a broadcast.  With them the score gathers (lanes = 16 queries
@@ -142,7 +148,7 @@ struct RelLayout {
   static constexpr int CW_LD = NCC == 5 ? 88 : 16 * NCC + 4;  // Cw[wave][QW][CW_LD]
   static constexpr int PW_LD = 16 * NPC + 20;                 // Pw[BN][PW_LD]
 
-  static constexpr int VT_SIZE = D * VT_LD;             // elements of one V^T buffer
+  static constexpr int VT_SIZE = BN * VS_LD;            // elements of one V tile buffer
 
   static constexpr size_t ks_off = 0;
   static constexpr size_t vt_off = ks_off + size_t(BN) * KS_LD * sizeof(T);
@@ -166,9 +172,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   constexpr int CPR = D / 8;            // 16-byte chunks per K row
   constexpr int NKC = BN * CPR;                  // 16-byte K chunks per tile
   constexpr int NCH = (NKC + kThreads - 1) / kThreads;
-  constexpr int VQD = D / 4;                     // 4-dim quads per V row
-  constexpr int NVBT = (BN / 4) * VQD;           // 4x4 V blocks per tile
-  constexpr int NVB = (NVBT + kThreads - 1) / kThreads;
+  constexpr int NVB = NCH;                       // 16-byte V chunks per thread (as K)
   constexpr int NCC = LY::NCC;
   constexpr int PU = LY::PU;
   constexpr int NPC = LY::NPC;
@@ -176,7 +180,6 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   static_assert(BN % 32 == 0 && BN <= 64, "key tile must be 32 or 64 keys");
   static_assert(QW % 16 == 0, "query rows per wavefront must be a multiple of 16");
   static_assert(NKC % kThreads == 0 || NKC < kThreads, "K tile must split evenly over the workgroup");
-  static_assert(NVBT % kThreads == 0 || NVBT < kThreads, "V tile must split evenly over the workgroup");
 
   extern __shared__ __align__(16) unsigned char smem[];
   T* Ks = reinterpret_cast<T*>(smem + LY::ks_off);
@@ -334,17 +337,14 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     koff[n] = static_cast<uint32_t>(r) * sl_bytes + cc * 16;
     kls[n] = static_cast<uint32_t>(r * LY::KS_LD + cc * 8);
   }
-  uint32_t voff[NVB];
+  // V chunks: the same rows and 16-byte chunks as K.
   uint32_t vls[NVB];
 #pragma unroll
   for (int n = 0; n < NVB; ++n) {
     const int t = tid + n * kThreads;
-    const int kq = t / VQD;
-    const int dq = t - kq * VQD;
-    // Thread block kq of a 16-key group holds keys kq%4 + {0, 4, 8, 12}, which
-    // land in V^T columns 4*(kq%4) + {0..3} (see key_of below).
-    voff[n] = static_cast<uint32_t>(16 * (kq / 4) + kq % 4) * sl_bytes + dq * 4 * ES;
-    vls[n] = static_cast<uint32_t>(4 * dq * LY::VT_LD + 4 * kq);
+    const int r = t / CPR;
+    const int cc = t - r * CPR;
+    vls[n] = static_cast<uint32_t>(r * LY::VS_LD + cc * 8);
   }
 
   // ---- relative windows ----
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   // ---- prefetch registers (K, V, mask of the next tile) ----
   u32x4_t pk[NCH];
-  u32x2_t pv[NVB][4];
+  u32x4_t pv[NVB];
   uint8_t pmask = 0;
   auto prefetch_k = [&](int j0) {
     const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
@@ -404,14 +404,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
 #pragma unroll
     for (int n = 0; n < NVB; ++n)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        if (NVBT >= kThreads || tid < NVBT) pv[n][rr] = load8(rv, voff[n] + jb + 4 * rr * sl_bytes);
+      if (NKC >= kThreads || tid < NKC) pv[n] = load16(rv, koff[n] + jb);
   };
 
   // ---- staging and window helpers ----
   // K of tile n+1 is staged right after the p2c barrier of tile n (every
-  // wavefront has finished reading K of tile n).  V^T has two placements:
+  // wavefront has finished reading K of tile n).  The V tile has two placements:
   //   * two buffers: V of tile n+1 goes into the other buffer at the same
   //     point, while tile n still reads its own;
   //   * one buffer: V of tile n is staged after the first barrier of tile n
@@ -422,22 +420,16 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     for (int n = 0; n < NCH; ++n)
       if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
   };
-  auto stage_v = [&](T* vt) {
+  // V rows are 8-byte aligned only (VS_LD = D + 4): two 8-byte stores per chunk.
+  auto stage_v = [&](T* vs) {
 #pragma unroll
-    for (int n = 0; n < NVB; ++n) {
-      if (NVBT < kThreads && tid >= NVBT) break;
-      Quad<T> rows[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) rows[rr] = __builtin_bit_cast(Quad<T>, pv[n][rr]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Quad<T> col;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) col[rr] = rows[rr][e];
-        *reinterpret_cast<Quad<T>*>(vt + vls[n] + e * LY::VT_LD) = col;
+    for (int n = 0; n < NVB; ++n)
+      if (NKC >= kThreads || tid < NKC) {
+        *reinterpret_cast<u32x2_t*>(vs + vls[n]) = u32x2_t{pv[n][0], pv[n][1]};
+        *reinterpret_cast<u32x2_t*>(vs + vls[n] + 4) = u32x2_t{pv[n][2], pv[n][3]};
       }
-    }
   };
+
   // c2p window of a tile: the kSlide new chunks are multiplied from crow (the
   // products stay in registers until the previous tile's gathers are done),
   // the kCarry old ones come from ccar.
@@ -773,15 +765,19 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const T* vrow = vt_cur + (16 * db + c) * LY::VT_LD + 32 * ks + 4 * g;
-        const Quad<T> lo = *reinterpret_cast<const Quad<T>*>(vrow);
-        const Quad<T> hi = *reinterpret_cast<const Quad<T>*>(vrow + 16);
-        F a;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          a[r] = lo[r];
-          a[4 + r] = hi[r];
-        }
+        // Transposing reads: lane c of group g supplies row 32ks + 4(c>>2) + g
+        // (+16 for the upper half), columns 16db + 4(c&3) .. +3, and receives
+        // V[rows of its k-slice][16db + c] -- keys g + 4e and 16 + g + 4e,
+        // the order of the P^T operand.
+        const T* p_lo = vt_cur + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
+        const T* p_hi = p_lo + 16 * LY::VS_LD;
+        // (The result is moved as whole dwords: assembling the operand from its
+        // 16-bit elements was compiled into wrong code.)
+        const u32x2_t lo = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
+        const u32x2_t hi = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
+        const F a = __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
       }
@@ -830,8 +826,8 @@ template <int D>
 constexpr int rel_block_n() {
   return 64;
 }
-// V^T buffers in LDS and workgroups per CU the registers are budgeted for.
-// d = 128 keeps one V^T buffer so that two workgroups fit in the LDS of a CU
+// V tile buffers in LDS and workgroups per CU the registers are budgeted for.
+// d = 128 keeps one V buffer so that two workgroups fit in the LDS of a CU
 // (65 KB each instead of 82 KB): 153 -> 117 us at B=16, L=512, H=8, fp16.
 // For d <= 64 (two workgroups either way) both placements time the same.
 template <int D>
