@@ -1,6 +1,6 @@
 """Benchmark of the fused DeBERTa disentangled-attention hot path on one MI355X.
 
-Headline (BASELINE.json ``metric``): fused attention TFLOP/s and fraction of the
+Headline metric: fused attention TFLOP/s and fraction of the
 fp16 dense MFMA peak at the attention microbench configuration
 (B=32, L=512, H=12, d=64, c2p|p2c, position_buckets=256, max_rel=512), plus the
 12-layer encoder latency at B=32, L=512 fp16 for the ``hip`` and the torch
@@ -45,7 +45,7 @@ def log(message: str) -> None:
 def c2_inputs(dtype: torch.dtype, padded: bool, seed: int = 2024, batch: int = 32,
               heads: int = 12, length: int = 512, dim: int = 64, device: str = "cuda",
               valid_lengths=None):
-    """Q/K/V and Qr/Kr ~ N(0,1)/sqrt(d); lengths U[256, 512] or none."""
+    """Attention microbenchmark inputs: Q/K/V and Qr/Kr ~ N(0,1)/sqrt(d); lengths U[256, 512] or none."""
 
     from disentangled_flash.position import compact_position_plan
 
@@ -457,7 +457,7 @@ def main() -> int:
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
-              "(see DESIGN.md for how the attention shards across GPUs); use --gpus 1.",
+              "(the attention grid shards over batch and heads with no exchange); use --gpus 1.",
               file=sys.stderr)
         return 2
     if not torch.cuda.is_available():

@@ -151,7 +151,7 @@ def test_table_kernel_matches_reference(dtype, mode):
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("pattern", ["right", "none"])
 def test_c2_full_size(dtype, pattern):
-    """B=32, L=512, H=12, d=64, Q/K/V/Qr/Kr ~ N(0,1)/sqrt(d)."""
+    """Attention microbenchmark shape: B=32, L=512, H=12, d=64, Q/K/V/Qr/Kr ~ N(0,1)/sqrt(d)."""
 
     gen = torch.Generator().manual_seed(2024)
     b, h, length, d = 32, 12, 512, 64

@@ -87,7 +87,7 @@ def _run_pair(hf_module, hip_module, states, rel, mask, dtype):
 @pytest.mark.parametrize("dtype", list(DTYPES))
 @pytest.mark.parametrize("mode", ["fused", "table"])
 def test_c1_layer_matches_huggingface(dtype, mode):
-    """BASELINE config 1 shape: v3-base layer, B=2, L=128, lengths U[64, 128]."""
+    """Single v3-base layer, B=2, L=128, lengths U[64, 128] (the CPU-runnable configuration)."""
 
     torch_dtype = DTYPES[dtype]
     hf_module, cfg = _hf_attention(768, 12, 64, ("c2p", "p2c"))
@@ -109,7 +109,7 @@ def test_c1_layer_matches_huggingface(dtype, mode):
 @pytest.mark.parametrize("mode", list(MODES))
 @pytest.mark.parametrize("shape", ["d128", "d32"])
 def test_c5_edge_sweep(dtype, mode, shape):
-    """d=128/H=8 at B=16 L=512 and d=32/H=16 at B=16 L=384."""
+    """Head-dim edge sweep: d=128/H=8 at B=16 L=512 and d=32/H=16 at B=16 L=384."""
 
     heads, head_dim, length = (8, 128, 512) if shape == "d128" else (16, 32, 384)
     torch_dtype = DTYPES[dtype]
@@ -161,7 +161,7 @@ def _encoder_inputs(batch, length, hidden, seed=19):
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 def test_12_layer_encoder_matches_huggingface(dtype):
-    """BASELINE config 3 architecture at B=8, L=256: final hidden states vs HF.
+    """12-layer base-shaped encoder at B=8, L=256: final hidden states vs HF.
 
     The HIP encoder in ``dtype`` must stay as close to the float32 HF encoder as
     HF's own encoder in ``dtype`` does (within 1.5x + the attention tolerance);
@@ -196,7 +196,7 @@ def test_12_layer_encoder_matches_huggingface(dtype):
 
 
 def test_xlarge_bf16_buckets():
-    """BASELINE config 4 (shortened to 4 layers): hidden 1536, 24 heads, bf16, buckets."""
+    """xlarge-shaped encoder (shortened to 4 layers): hidden 1536, 24 heads, bf16, buckets."""
 
     from disentangled_flash import enable_deberta_inference
 
