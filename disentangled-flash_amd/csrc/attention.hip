@@ -580,10 +580,8 @@ int launch(const Params& base, hipStream_t stream) {
   Params prm = base;
   prm.nqb = (prm.L + LY::kBlockM - 1) / LY::kBlockM;
   const size_t lds = LY::bytes(WINDOWED);
-  auto kernel = attention_kernel<T, D, BN, QW, C2P, P2C, TABLE>;
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(lds));
+  constexpr auto kernel = attention_kernel<T, D, BN, QW, C2P, P2C, TABLE>;
+  hipError_t err = ensure_dynamic_lds<kernel>(static_cast<int>(lds));
   if (err != hipSuccess) return static_cast<int>(err);
   const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H;
   if (blocks > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;

@@ -2,6 +2,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stdint.h>
 
 namespace dflash {
@@ -199,6 +201,22 @@ __device__ inline void store_quad(T* dst, f32x4_t acc) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) q[r] = to_t<T>(acc[r]);
   *reinterpret_cast<Quad<T>*>(dst) = q;
+}
+
+// Host: raise a kernel's dynamic LDS limit once per device (the attribute
+// persists), instead of on every launch.
+template <auto Kernel>
+inline hipError_t ensure_dynamic_lds(int bytes) {
+  static std::atomic<uint64_t> done{0};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const uint64_t bit = dev < 64 ? (uint64_t{1} << dev) : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+  err = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (err == hipSuccess && bit != 0) done.fetch_or(bit, std::memory_order_release);
+  return err;
 }
 
 }  // namespace dflash

@@ -848,10 +848,8 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   using LY = RelLayout<T, D, QW, BN, VB>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
-  auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C>;
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(LY::bytes));
+  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C>;
+  hipError_t err = ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
   if (err != hipSuccess) return static_cast<int>(err);
   const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H;
   if (blocks > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;
