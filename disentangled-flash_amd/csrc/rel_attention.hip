@@ -42,8 +42,8 @@
 // Mask semantics (kernel.py:250-261): kept query & kept key -> score; padded
 // query in range -> uniform over in-range keys; kept query & padded key ->
 // excluded; query past L -> first visited key only (row never stored).  The
-// key loop of a workgroup visits only the tiles between the first and last kept
-// key of the sequence; padded rows are stored as the mean of V.
+// key loop of a workgroup ends at the tile of the last kept key of the
+// sequence; padded rows are stored as the mean of V.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -218,59 +218,23 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   const auto rlut = make_rsrc(p.lut, static_cast<uint32_t>(2 * L - 1) * 4u);
 
   // ---- queries: fragments stay in registers (B operand of K.Q^T and Kr.Q^T) ----
+  // They are loaded in the prologue, after the lookups and rows that the first
+  // products wait for (loads return in issue order).
   F qf[kQB][KD];
   bool qkept[kQB];
   bool qin[kQB];
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    const int i = i0w + 16 * qb + c;
-#pragma unroll
-    for (int kd = 0; kd < KD; ++kd)
-      qf[qb][kd] = as_frag<T>(load16(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
-    qin[qb] = i < L;
-    qkept[qb] = load1(rmask, static_cast<uint32_t>(i)) != 0;  // zero past L
-  }
-  bool wave_all_kept = true;
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) wave_all_kept = wave_all_kept && __all(qkept[qb]);
 
   // ---- padding extent (wavefront-uniform; every wavefront derives the same values) ----
   // A kept query attends to kept keys only, so the key loop of a workgroup
-  // with kept queries is trimmed to the 64-key tiles from the first to the
-  // last kept key of the sequence.  A padded query in range attends uniformly
-  // to all L keys: its output is the mean of V over the sequence, which does
-  // not depend on the query and is computed separately (v_mean below).
-  bool wg_kept = false;
-  bool wg_padded = false;
-#pragma unroll
-  for (int q0 = 0; q0 < BM; q0 += 64) {
-    const int i = i0 + q0 + lane;
-    const bool mine = q0 + lane < BM;
-    const bool kept = mine && load1(rmask, static_cast<uint32_t>(i)) != 0;
-    wg_kept = wg_kept || __any(kept);
-    wg_padded = wg_padded || __any(mine && i < L && !kept);
-  }
-  int kfirst = 0;
-  int klast = L - 1;
-  if (wg_kept) {
-    kfirst = L;
-    klast = -1;
-    for (int base = 0; base < L; base += 256) {
-      uint8_t km[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) km[e] = load1(rmask, static_cast<uint32_t>(base + 64 * e + lane));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint64_t bits = __ballot(km[e] != 0);
-        if (bits != 0) {
-          kfirst = min(kfirst, base + 64 * e + __builtin_ctzll(bits));
-          klast = max(klast, base + 64 * e + 63 - __builtin_clzll(bits));
-        }
-      }
-    }
-  }
-  const int jstart = (kfirst / BN) * BN;
-  const int jend = klast + 1;
+  // with kept queries ends at the 64-key tile holding the last kept key of the
+  // sequence.  The loop always starts at key 0: the start is then known before
+  // any mask byte arrives, the lookup and K/V loads of the first tiles are
+  // issued without waiting for the scan, and the scan's loads are only waited
+  // for at the first loop test.  (Leading padded keys are excluded by the
+  // masking like any other padded key.)  A padded query in range attends
+  // uniformly to all L keys: its output is the mean of V over the sequence,
+  // which does not depend on the query and is computed separately (v_mean below).
+  constexpr int jstart = 0;
 
   // Mean of V over the L keys of (b, h) in fp32, left in LDS at vmean[0..D).
   float* vred = reinterpret_cast<float*>(smem);
@@ -287,15 +251,14 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
     };
-    int j = rg;
-    for (; j + 3 * RG < L; j += 4 * RG) {
-      u32x4_t raw[4];
+    // Eight rows in flight per step; rows past L read as zero and add nothing.
+    for (int j = rg; j < L; j += 8 * RG) {
+      u32x4_t raw[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) raw[u] = load16(rv, static_cast<uint32_t>(j + u * RG) * sl_bytes + cc * 16);
+      for (int u = 0; u < 8; ++u) raw[u] = load16(rv, static_cast<uint32_t>(j + u * RG) * sl_bytes + cc * 16);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) add_row(raw[u]);
+      for (int u = 0; u < 8; ++u) add_row(raw[u]);
     }
-    for (; j < L; j += RG) add_row(load16(rv, static_cast<uint32_t>(j) * sl_bytes + cc * 16));
     lds_barrier();  // LDS of the key loop no longer read
 #pragma unroll
     for (int e = 0; e < 8; ++e) vred[tid * 8 + e] = acc[e];
@@ -312,19 +275,6 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   T* outp = reinterpret_cast<T*>(p.out);
   const int64_t row_stride = static_cast<int64_t>(p.H) * D;
-  if (!wg_kept) {
-    // Every query of the workgroup is padded (or past L): all rows are the mean of V.
-    v_mean();
-    const int row_lo = i0 + tid / (D / 4);
-    for (int i = row_lo; i < min(i0 + BM, L); i += kThreads / (D / 4)) {
-      const int d0 = 4 * (tid % (D / 4));
-      Quad<T> q;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[d0 + r]);
-      *reinterpret_cast<Quad<T>*>(outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + d0) = q;
-    }
-    return;
-  }
 
   // ---- per-thread offsets of the K / V tile loads (add j0 * row stride per tile) ----
   uint32_t koff[NCH];
@@ -393,19 +343,21 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   u32x4_t pk[NCH];
   u32x4_t pv[NVB];
   uint8_t pmask = 0;
-  auto prefetch_k = [&](int j0) {
+  auto prefetch_k_into = [&](int j0, u32x4_t (&dk)[NCH], uint8_t& dm) {
     const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
 #pragma unroll
     for (int n = 0; n < NCH; ++n)
-      if (NKC >= kThreads || tid < NKC) pk[n] = load16(rk, koff[n] + jb);
-    pmask = load1(rmask, static_cast<uint32_t>(j0 + lane));
+      if (NKC >= kThreads || tid < NKC) dk[n] = load16(rk, koff[n] + jb);
+    dm = load1(rmask, static_cast<uint32_t>(j0 + lane));
   };
-  auto prefetch_v = [&](int j0) {
+  auto prefetch_v_into = [&](int j0, u32x4_t (&dv)[NVB]) {
     const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
 #pragma unroll
     for (int n = 0; n < NVB; ++n)
-      if (NKC >= kThreads || tid < NKC) pv[n] = load16(rv, koff[n] + jb);
+      if (NKC >= kThreads || tid < NKC) dv[n] = load16(rv, koff[n] + jb);
   };
+  auto prefetch_k = [&](int j0) { prefetch_k_into(j0, pk, pmask); };
+  auto prefetch_v = [&](int j0) { prefetch_v_into(j0, pv); };
 
   // ---- staging and window helpers ----
   // K of tile n+1 is staged right after the p2c barrier of tile n (every
@@ -486,52 +438,170 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   };
 
-  // ---- prologue: windows and K/V of tile 0 ----
+  // ---- prologue: loads of tile 0, in the order their results are needed ----
+  // Lookups first (they depend only on the block).
+  int lc[C2P ? NCC : 1];
+  int lp[P2C ? PU : 1];
   if constexpr (C2P) {
-    int lc[NCC];
 #pragma unroll
     for (int ch = 0; ch < NCC; ++ch) lc[ch] = lut_load(lut_c_index(jstart, ch));
-#pragma unroll
-    for (int ch = 0; ch < kSlide; ++ch)
-#pragma unroll
-      for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = row_frag(rkr, lc[ch], kd);
-#pragma unroll
-    for (int ch = 0; ch < kCarry; ++ch) {
-      F r0[KD];
-#pragma unroll
-      for (int kd = 0; kd < KD; ++kd) r0[kd] = row_frag(rkr, lc[kSlide + ch], kd);
-#pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) {
-        f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd) acc = M::run(r0[kd], qf[qb][kd], acc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ccar[ch][qb][r] = static_cast<T>(acc[r]);
-      }
-    }
 #pragma unroll
     for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(jstart + BN, ch));
   }
   if constexpr (P2C) {
 #pragma unroll
-    for (int u = 0; u < PU; ++u) {
-      const int lp = lut_load(lut_p_index(jstart, u));
-#pragma unroll
-      for (int kd = 0; kd < KD; ++kd) prow[u][kd] = row_frag(rqr, lp, kd);
-    }
+    for (int u = 0; u < PU; ++u) lp[u] = lut_load(lut_p_index(jstart, u));
     lutp = lut_load(lut_p_index(jstart + BN, 0));
+  }
+  // Mask bytes: the first 512 of the sequence (for the extent), the
+  // workgroup's queries and each lane's queries.  Bytes past L read as zero.
+  uint8_t km[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) km[e] = load1(rmask, static_cast<uint32_t>(64 * e + lane));
+  constexpr int kWgMaskLoads = (BM + 63) / 64;
+  uint8_t wm[kWgMaskLoads];
+#pragma unroll
+  for (int n = 0; n < kWgMaskLoads; ++n)
+    wm[n] = 64 * n + lane < BM ? load1(rmask, static_cast<uint32_t>(i0 + 64 * n + lane)) : 0;
+  uint8_t qm[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) qm[qb] = load1(rmask, static_cast<uint32_t>(i0w + 16 * qb + c));
+
+  // Rows of the tile-0 windows (they wait only for the lookups above), then Q
+  // and the K/V of tile 0.
+  F r0[C2P && kCarry > 0 ? kCarry : 1][KD];
+  if constexpr (C2P) {
+#pragma unroll
+    for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = row_frag(rkr, lc[ch], kd);
+#pragma unroll
+    for (int ch = 0; ch < kCarry; ++ch)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) r0[ch][kd] = row_frag(rkr, lc[kSlide + ch], kd);
+  }
+  if constexpr (P2C) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) prow[u][kd] = row_frag(rqr, lp[u], kd);
+  }
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    const int i = i0w + 16 * qb + c;
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd)
+      qf[qb][kd] = as_frag<T>(load16(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
+    qin[qb] = i < L;
   }
   prefetch_k(jstart);
   prefetch_v(jstart);
+  // Tile 1 (d <= 64; d = 128 has no registers to spare here): K/V and the
+  // rows of its new c2p chunks (lookups in lutc), moved into the pipeline
+  // registers once tile 0 has been staged and multiplied.
+  constexpr bool kEarlyTile1 = D <= 64;
+  u32x4_t pk1[NCH];
+  u32x4_t pv1[NVB];
+  uint8_t pmask1 = 0;
+  F crow1[C2P && kEarlyTile1 ? kSlide : 1][KD];
+  if constexpr (kEarlyTile1) {
+    prefetch_k_into(jstart + BN, pk1, pmask1);
+    if constexpr (VBUFS == 2) prefetch_v_into(jstart + BN, pv1);
+  }
+  if constexpr (C2P && kEarlyTile1) {
+#pragma unroll
+    for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) crow1[ch][kd] = row_frag(rkr, lutc[ch], kd);
+  }
+
+  // Extent and query flags from the mask bytes.
+  bool wg_kept = false;
+  bool wg_padded = false;
+#pragma unroll
+  for (int n = 0; n < kWgMaskLoads; ++n) {
+    const bool mine = 64 * n + lane < BM;
+    const bool kept = wm[n] != 0;
+    wg_kept = wg_kept || __any(kept);
+    wg_padded = wg_padded || __any(mine && i0 + 64 * n + lane < L && !kept);
+  }
+  int klast = -1;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint64_t bits = __ballot(km[e] != 0);
+    if (bits != 0) klast = 64 * e + 63 - __builtin_clzll(bits);
+  }
+  for (int base = 512; base < L; base += 512) {  // sequences longer than 512
+#pragma unroll
+    for (int e = 0; e < 8; ++e) km[e] = load1(rmask, static_cast<uint32_t>(base + 64 * e + lane));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint64_t bits = __ballot(km[e] != 0);
+      if (bits != 0) klast = base + 64 * e + 63 - __builtin_clzll(bits);
+    }
+  }
+  const int jend = klast + 1;  // a kept query's own key is kept: klast >= 0 when wg_kept
+  bool wave_all_kept = true;
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    qkept[qb] = qm[qb] != 0;
+    wave_all_kept = wave_all_kept && __all(qkept[qb]);
+  }
+
+  if (!wg_kept) {
+    // Every query of the workgroup is padded (or past L): all rows are the mean of V.
+    v_mean();
+    const int row_lo = i0 + tid / (D / 4);
+    for (int i = row_lo; i < min(i0 + BM, L); i += kThreads / (D / 4)) {
+      const int d0 = 4 * (tid % (D / 4));
+      Quad<T> q;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[d0 + r]);
+      *reinterpret_cast<Quad<T>*>(outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + d0) = q;
+    }
+    return;
+  }
+
+  // ---- prologue: carried c2p chunks of tile 0 ----
+  if constexpr (C2P) {
+#pragma unroll
+    for (int ch = 0; ch < kCarry; ++ch)
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+        f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) acc = M::run(r0[ch][kd], qf[qb][kd], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ccar[ch][qb][r] = static_cast<T>(acc[r]);
+      }
+  }
   stage_k();
   if constexpr (VBUFS == 2) stage_v(Vt);
   uint64_t kept_cur = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
   uint64_t kept_next = 0;
   c2p_products();
   c2p_store();
-  prefetch_k(jstart + BN);
-  if constexpr (VBUFS == 2) prefetch_v(jstart + BN);
-  load_crow(jstart + BN);
+  if constexpr (kEarlyTile1) {
+#pragma unroll
+    for (int n = 0; n < NCH; ++n) pk[n] = pk1[n];
+    pmask = pmask1;
+    if constexpr (VBUFS == 2) {
+#pragma unroll
+      for (int n = 0; n < NVB; ++n) pv[n] = pv1[n];
+    }
+    if constexpr (C2P) {
+#pragma unroll
+      for (int ch = 0; ch < kSlide; ++ch) {
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) crow[ch][kd] = crow1[ch][kd];
+        lutc[ch] = lut_load(lut_c_index(jstart + 2 * BN, ch));
+      }
+    }
+  } else {
+    prefetch_k(jstart + BN);
+    if constexpr (VBUFS == 2) prefetch_v(jstart + BN);
+    load_crow(jstart + BN);
+  }
 
   // ---- accumulators ----
   f32x4_t o[DB][kQB];
