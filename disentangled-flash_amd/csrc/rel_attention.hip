@@ -39,11 +39,11 @@
 // and read as slot 0 (those elements are masked or belong to rows that are
 // never stored).  Offsets are never negative.
 //
-// Mask semantics (kernel.py:250-261): kept query & kept key -> score; padded
-// query in range -> uniform over in-range keys; kept query & padded key ->
-// excluded; query past L -> first visited key only (row never stored).  The
-// key loop of a workgroup ends at the tile of the last kept key of the
-// sequence; padded rows are stored as the mean of V.
+// Mask semantics (kernel.py:250-261): kept query & kept key -> score; kept
+// query & padded key -> excluded; padded query in range -> uniform over the
+// in-range keys, i.e. the mean of V, which is computed separately and stored
+// for those rows.  The key loop of a workgroup ends at the tile of the last
+// kept key of the sequence.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -222,7 +222,6 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // products wait for (loads return in issue order).
   F qf[kQB][KD];
   bool qkept[kQB];
-  bool qin[kQB];
 
   // ---- padding extent (wavefront-uniform; every wavefront derives the same values) ----
   // A kept query attends to kept keys only, so the key loop of a workgroup
@@ -492,7 +491,6 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd)
       qf[qb][kd] = as_frag<T>(load16(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
-    qin[qb] = i < L;
   }
   prefetch_k(jstart);
   prefetch_v(jstart);
@@ -541,12 +539,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   }
   const int jend = klast + 1;  // a kept query's own key is kept: klast >= 0 when wg_kept
-  bool wave_all_kept = true;
 #pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) {
-    qkept[qb] = qm[qb] != 0;
-    wave_all_kept = wave_all_kept && __all(qkept[qb]);
-  }
+  for (int qb = 0; qb < kQB; ++qb) qkept[qb] = qm[qb] != 0;
 
   if (!wg_kept) {
     // Every query of the workgroup is padded (or past L): all rows are the mean of V.
@@ -752,26 +746,23 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           }
     }
 
-    // ---- masking (wavefront-uniform slow path) ----
+    // ---- masking (wavefront-uniform slow path: tiles with a padded key or past L) ----
+    // Every row drops the padded keys.  That is the rule for kept queries; the
+    // other rows are never stored from the accumulators (a padded query in
+    // range takes the mean of V, a query past L is not stored), so they only
+    // have to stay finite or empty, which they do: every row of a workgroup
+    // with a kept query meets at least one kept key.
     constexpr uint64_t kTileBits = BN == 64 ? ~uint64_t{0} : (uint64_t{1} << (BN % 64)) - 1;
     const bool full_tile = (j0 + BN <= L) && (kept_cur & kTileBits) == kTileBits;
-    if (!(full_tile && wave_all_kept)) {
+    if (!full_tile) {
       const uint64_t lane_bits = kept_cur >> g;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int j = j0 + 16 * kb + g + 4 * r;
           const bool key_kept = (lane_bits >> (16 * kb + 4 * r)) & 1;
 #pragma unroll
-          for (int qb = 0; qb < kQB; ++qb) {
-            // kept row: drop padded keys; padded row: uniform over in-range
-            // keys (replaced by the mean of V at the end); row past L: the
-            // first visited key only (never stored).
-            const bool hit = qkept[qb] ? key_kept : (qin[qb] ? j < L : j == jstart);
-            const float v = qkept[qb] ? sc[kb][qb][r] : 0.0f;
-            sc[kb][qb][r] = hit ? v : -INFINITY;
-          }
+          for (int qb = 0; qb < kQB; ++qb) sc[kb][qb][r] = key_kept ? sc[kb][qb][r] : -INFINITY;
         }
     }
 
