@@ -466,8 +466,35 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) qm[qb] = load1(rmask, static_cast<uint32_t>(i0w + 16 * qb + c));
 
-  // Rows of the tile-0 windows (they wait only for the lookups above), then Q
-  // and the K/V of tile 0.
+  // Workgroup and query flags from the mask bytes.
+  bool wg_kept = false;
+  bool wg_padded = false;
+#pragma unroll
+  for (int n = 0; n < kWgMaskLoads; ++n) {
+    const bool mine = 64 * n + lane < BM;
+    const bool kept = wm[n] != 0;
+    wg_kept = wg_kept || __any(kept);
+    wg_padded = wg_padded || __any(mine && i0 + 64 * n + lane < L && !kept);
+  }
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) qkept[qb] = qm[qb] != 0;
+
+  if (!wg_kept) {
+    // Every query of the workgroup is padded (or past L): all rows are the mean of V.
+    v_mean();
+    const int row_lo = i0 + tid / (D / 4);
+    for (int i = row_lo; i < min(i0 + BM, L); i += kThreads / (D / 4)) {
+      const int d0 = 4 * (tid % (D / 4));
+      Quad<T> q;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[d0 + r]);
+      *reinterpret_cast<Quad<T>*>(outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + d0) = q;
+    }
+    return;
+  }
+
+  // Rows of the tile-0 windows, then Q and the K/V of tile 0 (a workgroup
+  // without kept queries has left before issuing them).
   F r0[C2P && kCarry > 0 ? kCarry : 1][KD];
   if constexpr (C2P) {
 #pragma unroll
@@ -513,16 +540,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       for (int kd = 0; kd < KD; ++kd) crow1[ch][kd] = row_frag(rkr, lutc[ch], kd);
   }
 
-  // Extent and query flags from the mask bytes.
-  bool wg_kept = false;
-  bool wg_padded = false;
-#pragma unroll
-  for (int n = 0; n < kWgMaskLoads; ++n) {
-    const bool mine = 64 * n + lane < BM;
-    const bool kept = wm[n] != 0;
-    wg_kept = wg_kept || __any(kept);
-    wg_padded = wg_padded || __any(mine && i0 + 64 * n + lane < L && !kept);
-  }
+  // Last kept key (the loop bound) from the mask bytes loaded above.
   int klast = -1;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -539,22 +557,6 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   }
   const int jend = klast + 1;  // a kept query's own key is kept: klast >= 0 when wg_kept
-#pragma unroll
-  for (int qb = 0; qb < kQB; ++qb) qkept[qb] = qm[qb] != 0;
-
-  if (!wg_kept) {
-    // Every query of the workgroup is padded (or past L): all rows are the mean of V.
-    v_mean();
-    const int row_lo = i0 + tid / (D / 4);
-    for (int i = row_lo; i < min(i0 + BM, L); i += kThreads / (D / 4)) {
-      const int d0 = 4 * (tid % (D / 4));
-      Quad<T> q;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[d0 + r]);
-      *reinterpret_cast<Quad<T>*>(outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + d0) = q;
-    }
-    return;
-  }
 
   // ---- prologue: carried c2p chunks of tile 0 ----
   if constexpr (C2P) {
