@@ -24,14 +24,15 @@
 // then sits at a window index that is a lane constant plus a compile-time
 // offset, so the score gathers are LDS reads with immediate offsets and no
 // lookup table is touched inside the tile.  The price is that deltas sharing
-// a bucket are multiplied more than once, which costs MFMA cycles, of which
-// this kernel has spare (its bound is VALU).
+// a bucket are multiplied more than once (about 15 % more relative-score MFMA
+// work than one product per slot).
 //
 // Layout of the score tile: S^T = K.Q^T with v_mfma_f32_16x16x32_{f16,bf16},
 // so each lane holds one query column and four keys per 16x16 block; the
 // probabilities are then already the B operand of O^T += V^T.P^T.
-// Row sums come from the same MFMA with an all-ones A operand, so no
-// cross-lane reduction is needed for them.
+// Row sums come from the same MFMA with an all-ones A operand (d <= 64), or
+// for d = 128, whose matrix unit is the busier one, from per-lane dot2 sums
+// reduced over the four lane groups at the end.
 //
 // Global reads go through buffer resources: an offset at or past the
 // resource's size returns zero, which clamps rows past L for free; lookup
@@ -114,6 +115,18 @@ __device__ inline float add2(float s, T a, T b) {
     const bf16x2_t v = {a, b};
     const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
     return __builtin_amdgcn_fdot2_f32_bf16(v, one, s, false);
+  }
+}
+
+// s + lo + hi of a packed pair of T (exact products with 1, fp32 sum).
+template <typename T>
+__device__ inline float sum2(float s, uint32_t packed) {
+  if constexpr (__is_same(T, _Float16)) {
+    const half2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, packed), one, s, false);
+  } else {
+    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, packed), one, s, false);
   }
 }
 
@@ -601,7 +614,10 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   // ---- accumulators ----
   f32x4_t o[DB][kQB];
-  f32x4_t rs[kQB];  // row sums (all four entries equal)
+  // Row sums: MFMA form (all four entries equal) or this lane's part (entry 0:
+  // its keys g + 4r of every block), see kRowSumValu.
+  constexpr bool kRowSumValu = D >= 128;
+  f32x4_t rs[kQB];
   float row_max[kQB];
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
@@ -824,7 +840,14 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           pf[qb][r] = static_cast<T>(sc[2 * ks][qb][r]);
           pf[qb][4 + r] = static_cast<T>(sc[2 * ks + 1][qb][r]);
         }
-        rs[qb] = M::run(ones, pf[qb], rs[qb]);
+        // Row sums of the rounded probabilities (the values PV multiplies).
+        if constexpr (kRowSumValu) {
+          const u32x4_t pp = __builtin_bit_cast(u32x4_t, pf[qb]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rs[qb][0] = sum2<T>(rs[qb][0], pp[e]);
+        } else {
+          rs[qb] = M::run(ones, pf[qb], rs[qb]);
+        }
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
@@ -854,12 +877,21 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   }
 
   // ---- normalise and store [B, L, H*D]; padded rows take the mean of V ----
+  float row_sum[kQB];
+#pragma unroll
+  for (int qb = 0; qb < kQB; ++qb) {
+    row_sum[qb] = rs[qb][0];
+    if constexpr (kRowSumValu) {
+      row_sum[qb] += __shfl_xor(row_sum[qb], 16);
+      row_sum[qb] += __shfl_xor(row_sum[qb], 32);
+    }
+  }
   if (wg_padded) v_mean();
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
     const int i = i0w + 16 * qb + c;
     if (i >= L) continue;
-    const float inv = 1.0f / rs[qb][0];
+    const float inv = 1.0f / row_sum[qb];
     T* dst = outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + 4 * g;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
