@@ -139,6 +139,18 @@ def test_rel_kernel_mask_patterns(pattern, dtype):
     _check(out, *args, True, True, pattern)
 
 
+@pytest.mark.parametrize("pattern", ["left", "heavy", "boundary", "holes"])
+@pytest.mark.parametrize("dim,heads", [(32, 3), (128, 2)])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_rel_kernel_mask_patterns_head_dims(pattern, dim, heads, dtype):
+    # Padded keys, padded query rows and partial tiles for the d = 32 and
+    # d = 128 instances (d = 128 keeps its row sums on the VALU).
+    args = _inputs(6, heads, 320, dim, DTYPES[dtype], pattern, seed=dim + 7)
+    for has_c2p, has_p2c in MODES.values():
+        out = _run_rel(*args, has_c2p, has_p2c)
+        _check(out, *args, has_c2p, has_p2c, f"{pattern} d={dim} c2p={has_c2p} p2c={has_p2c}")
+
+
 @pytest.mark.parametrize("dtype", list(DTYPES))
 @pytest.mark.parametrize("mode", ["both", "c2p", "p2c", "none"])
 def test_table_kernel_matches_reference(dtype, mode):
