@@ -772,7 +772,10 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     // with a kept query meets at least one kept key.
     constexpr uint64_t kTileBits = BN == 64 ? ~uint64_t{0} : (uint64_t{1} << (BN % 64)) - 1;
     const bool full_tile = (j0 + BN <= L) && (kept_cur & kTileBits) == kTileBits;
-    if (!full_tile) {
+    if (__builtin_expect(!full_tile, 0)) {
+      // (The empty asm keeps this a branch: if-converted, the selects would
+      // run on every tile.)
+      asm volatile("");
       const uint64_t lane_bits = kept_cur >> g;
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
