@@ -32,6 +32,7 @@
 //   query past L                    -> 0 at key 0 only (row never stored)
 
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <stdint.h>
 
 #include "dflash.h"
@@ -674,14 +675,33 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
   return dispatch<true>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
 }
 
-int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,
-                             int64_t stride_b, int64_t stride_h, int64_t stride_l,
-                             const void* pos_key, const void* pos_query,
-                             const int32_t* delta_to_local, const uint8_t* attention_mask,
-                             void* out, int B, int H, int L, int D, int S,
-                             float score_scale_log2, int has_c2p, int has_p2c, int dtype,
-                             int strict_fp32, void* stream) {
-  (void)strict_fp32;
+}  // extern "C"
+
+namespace {
+
+// CU count of the current device (cached per device).
+int current_device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int known = cache[dev].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  if (dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// Both relative-score entry points; splits <= 1 is the single-pass form.
+int rel_forward(const void* query, const void* key, const void* value, int64_t stride_b,
+                int64_t stride_h, int64_t stride_l, const void* pos_key, const void* pos_query,
+                const int32_t* delta_to_local, const uint8_t* attention_mask, void* out, int B,
+                int H, int L, int D, int S, float score_scale_log2, int has_c2p, int has_p2c,
+                int dtype, int splits, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_common(query, key, value, delta_to_local, attention_mask, out, B, H, L, D, S,
                         has_c2p, has_p2c, dtype);
   if (rc == kEmptyBatch) return DFLASH_OK;
@@ -718,6 +738,22 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
     rp.scale_log2 = score_scale_log2;
     rp.has_c2p = has_c2p;
     rp.has_p2c = has_p2c;
+    rp.splits = 1;
+    if (splits > 1) {
+      if (splits > 8) return DFLASH_ERR_SHAPE;
+      const int tiles = (L + 63) / 64;
+      const int st = (tiles + splits - 1) / splits;
+      const int eff = (tiles + st - 1) / st;
+      if (eff > 1) {
+        if (!workspace) return DFLASH_ERR_NULL;
+        if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return DFLASH_ERR_ALIGN;
+        if (workspace_bytes < rel_attention_workspace_bytes(eff, B, H, L, D))
+          return DFLASH_ERR_WORKSPACE;
+        rp.splits = eff;
+        rp.split_tiles = st;
+        rp.part = static_cast<float*>(workspace);
+      }
+    }
     return launch_rel_attention_16bit(rp, D, dtype, static_cast<hipStream_t>(stream));
   }
   Params prm{};
@@ -740,6 +776,54 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
   return dispatch<false>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
 }
 
+}  // namespace
+
+extern "C" {
+
+int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,
+                             int64_t stride_b, int64_t stride_h, int64_t stride_l,
+                             const void* pos_key, const void* pos_query,
+                             const int32_t* delta_to_local, const uint8_t* attention_mask,
+                             void* out, int B, int H, int L, int D, int S,
+                             float score_scale_log2, int has_c2p, int has_p2c, int dtype,
+                             int strict_fp32, void* stream) {
+  (void)strict_fp32;
+  return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
+                     delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
+                     has_c2p, has_p2c, dtype, 1, nullptr, 0, stream);
+}
+
+int dflash_attention_rel_split_plan(int B, int H, int L, int D, int* splits,
+                                    size_t* workspace_bytes) {
+  if (!splits || !workspace_bytes) return DFLASH_ERR_NULL;
+  if (B < 0 || H < 1 || L < 1) return DFLASH_ERR_SHAPE;
+  if (D != 32 && D != 64 && D != 128) return DFLASH_ERR_HEAD_DIM;
+  if (*splits > 8) return DFLASH_ERR_SHAPE;
+  if (*splits <= 0) {
+    *splits = rel_attention_splits(B, H, L, D, current_device_cus(), nullptr);
+  } else {  // the count the split form runs for this request
+    const int tiles = (L + 63) / 64;
+    const int st = (tiles + *splits - 1) / *splits;
+    *splits = (tiles + st - 1) / st;
+  }
+  *workspace_bytes = rel_attention_workspace_bytes(*splits, B, H, L, D);
+  return DFLASH_OK;
+}
+
+int dflash_attention_rel_fwd_split(const void* query, const void* key, const void* value,
+                                   int64_t stride_b, int64_t stride_h, int64_t stride_l,
+                                   const void* pos_key, const void* pos_query,
+                                   const int32_t* delta_to_local,
+                                   const uint8_t* attention_mask, void* out, int B, int H,
+                                   int L, int D, int S, float score_scale_log2, int has_c2p,
+                                   int has_p2c, int dtype, int strict_fp32, int splits,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  (void)strict_fp32;
+  return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
+                     delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
+                     has_c2p, has_p2c, dtype, splits, workspace, workspace_bytes, stream);
+}
+
 const char* dflash_error_string(int code) {
   switch (code) {
     case DFLASH_OK:
@@ -756,6 +840,8 @@ const char* dflash_error_string(int code) {
       return "tensors and strides must be 16-byte aligned";
     case DFLASH_ERR_TOO_LARGE:
       return "launch grid exceeds the device limit";
+    case DFLASH_ERR_WORKSPACE:
+      return "workspace smaller than dflash_attention_rel_split_plan reports";
     default:
       return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }

@@ -20,9 +20,23 @@ struct RelParams {
   int nqb;                   // query blocks per (b, h), set by the launcher
   float scale_log2;          // log2(e) / sqrt(d * factor)
   int has_c2p, has_p2c;
+  // Key splits (1 = none).  With splits > 1 each workgroup walks split_tiles
+  // key tiles and writes unnormalised partial rows to part (fp32 [splits, B,
+  // L, H, D], then {base, sum} pairs [splits, B, L, H]); a merge kernel
+  // combines them.
+  int splits;
+  int split_tiles;
+  float* part;
 };
 
 // fp16 / bf16, D in {32, 64, 128}; arguments already validated by the caller.
+// prm.splits / split_tiles / part select the split-key form (with its merge).
 int launch_rel_attention_16bit(const RelParams& prm, int D, int dtype, hipStream_t stream);
+
+// Key splits for a launch of B*H query-block rows that would leave the GPU
+// underfilled (fewer workgroups than two per CU), and the workspace bytes they
+// need; 1 and 0 when no split pays.
+int rel_attention_splits(int B, int H, int L, int D, int cus, int* split_tiles);
+size_t rel_attention_workspace_bytes(int splits, int B, int H, int L, int D);
 
 }  // namespace dflash

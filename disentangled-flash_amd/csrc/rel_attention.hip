@@ -207,7 +207,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   const int g = lane >> 4;
 
   const int L = p.L;
-  const int m = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int mk = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int split = mk % p.splits;  // key split (the splits of a block are neighbours)
+  const int m = mk / p.splits;
   const int bh = m / p.nqb;
   const int qblk = m - bh * p.nqb;
   const int b = bh / p.H;
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // masking like any other padded key.)  A padded query in range attends
   // uniformly to all L keys: its output is the mean of V over the sequence,
   // which does not depend on the query and is computed separately (v_mean below).
-  constexpr int jstart = 0;
+  const int jstart = split * p.split_tiles * BN;  // 0 without splits
 
   // Mean of V over the L keys of (b, h) in fp32, left in LDS at vmean[0..D).
   float* vred = reinterpret_cast<float*>(smem);
@@ -493,6 +495,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   for (int qb = 0; qb < kQB; ++qb) qkept[qb] = qm[qb] != 0;
 
   if (!wg_kept) {
+    if (split > 0) return;  // split 0 stores the mean of V
     // Every query of the workgroup is padded (or past L): all rows are the mean of V.
     v_mean();
     const int row_lo = i0 + tid / (D / 4);
@@ -569,7 +572,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       if (bits != 0) klast = base + 64 * e + 63 - __builtin_clzll(bits);
     }
   }
-  const int jend = klast + 1;  // a kept query's own key is kept: klast >= 0 when wg_kept
+  // A kept query's own key is kept: klast >= 0 when wg_kept.
+  const int jend = p.splits > 1 ? min(klast + 1, jstart + p.split_tiles * BN) : klast + 1;
 
   // ---- prologue: carried c2p chunks of tile 0 ----
   if constexpr (C2P) {
@@ -889,6 +893,38 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       row_sum[qb] += __shfl_xor(row_sum[qb], 32);
     }
   }
+  if (p.splits > 1) {
+    // Partial rows of this key split: unnormalised O, the exponent base and
+    // the row sum (the merge kernel combines the splits of kept rows).  Split 0
+    // also stores the padded rows, which do not depend on the keys.
+    if (split == 0 && wg_padded) v_mean();
+    const int64_t rows = static_cast<int64_t>(p.B) * L * p.H;
+    float* part_o = p.part;
+    float2* part_ml = reinterpret_cast<float2*>(p.part + static_cast<int64_t>(p.splits) * rows * D);
+#pragma unroll
+    for (int qb = 0; qb < kQB; ++qb) {
+      const int i = i0w + 16 * qb + c;
+      if (i >= L) continue;
+      const int64_t row = (static_cast<int64_t>(split) * p.B + b) * L * p.H +
+                          static_cast<int64_t>(i) * p.H + h;
+      if (qkept[qb]) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          *reinterpret_cast<f32x4_t*>(part_o + row * D + 16 * db + 4 * g) = o[db][qb];
+        if (g == 0) part_ml[row] = float2{row_max[qb], row_sum[qb]};
+      } else if (split == 0) {
+        T* dst = outp + (static_cast<int64_t>(b) * L + i) * row_stride + h * D + 4 * g;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          Quad<T> q;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(vmean[16 * db + 4 * g + r]);
+          *reinterpret_cast<Quad<T>*>(dst + 16 * db) = q;
+        }
+      }
+    }
+    return;
+  }
   if (wg_padded) v_mean();
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
@@ -937,6 +973,54 @@ constexpr int rel_workgroups_per_cu() {
   return 2;
 }
 
+constexpr int kMaxKeySplits = 8;
+
+// Merge of the key splits: per kept row (b, i, h), 4 output elements per thread,
+//   o = sum_s 2^(base_s - M) O_s / sum_s 2^(base_s - M) l_s,  M = max_s base_s
+// (a split that met no kept key has base -inf and l = 0, so weight 0).
+template <typename T>
+__global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __restrict__ part,
+                                                              const uint8_t* __restrict__ mask,
+                                                              T* __restrict__ out, int64_t rows,
+                                                              int H, int D, int splits) {
+  const int per_row = D / 4;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = t / per_row;
+  if (row >= rows) return;
+  if (mask[row / H] == 0) return;  // padded query: stored by split 0
+  const int d0 = 4 * static_cast<int>(t - row * per_row);
+  const float2* ml = reinterpret_cast<const float2*>(part + static_cast<int64_t>(splits) * rows * D);
+  // All loads first (at most eight splits), then one pass.
+  float2 v[kMaxKeySplits];
+  f32x4_t po[kMaxKeySplits];
+#pragma unroll
+  for (int sp = 0; sp < kMaxKeySplits; ++sp) {
+    if (sp < splits) {
+      v[sp] = ml[sp * rows + row];
+      po[sp] = *reinterpret_cast<const f32x4_t*>(part + (sp * rows + row) * D + d0);
+    }
+  }
+  float base = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < kMaxKeySplits; ++sp)
+    if (sp < splits) base = fmaxf(base, v[sp].x);
+  float l = 0.0f;
+  f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int sp = 0; sp < kMaxKeySplits; ++sp) {
+    if (sp < splits) {
+      const float w = __builtin_amdgcn_exp2f(v[sp].x - base);
+      l += w * v[sp].y;
+      acc += w * po[sp];
+    }
+  }
+  const float inv = 1.0f / l;
+  Quad<T> q;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) q[r] = static_cast<T>(acc[r] * inv);
+  *reinterpret_cast<Quad<T>*>(out + row * D + d0) = q;
+}
+
 template <typename T, int D, bool C2P, bool P2C>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int QW = rel_queries_per_wave<D>();
@@ -949,10 +1033,18 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C>;
   hipError_t err = ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
   if (err != hipSuccess) return static_cast<int>(err);
-  const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H;
+  if (prm.splits < 1) prm.splits = 1;
+  const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H * prm.splits;
   if (blocks > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), LY::bytes,
                      stream, prm);
+  err = hipGetLastError();
+  if (err != hipSuccess || prm.splits == 1) return static_cast<int>(err);
+  const int64_t rows = static_cast<int64_t>(prm.B) * prm.L * prm.H;
+  const int64_t threads = rows * (D / 4);
+  hipLaunchKernelGGL(rel_split_merge_kernel<T>, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                     dim3(256), 0, stream, static_cast<const float*>(prm.part), prm.mask,
+                     static_cast<T*>(prm.out), rows, prm.H, D, prm.splits);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -965,6 +1057,33 @@ int rel_modes(const RelParams& prm, hipStream_t stream) {
 }
 
 }  // namespace
+
+int rel_attention_splits(int B, int H, int L, int D, int cus, int* split_tiles) {
+  // Split only when the unsplit grid leaves most CUs idle (at most a quarter
+  // of them get a workgroup), and only up to one workgroup per CU: a workgroup
+  // costs about four tiles of fixed time (start-up, pipeline fill, partial
+  // rows), which only pays when the CUs it occupies would otherwise idle.
+  // Each split keeps at least two key tiles; at most eight splits.
+  const int bm = kWaves * (D >= 128 ? 16 : 32);
+  const int64_t blocks = static_cast<int64_t>((L + bm - 1) / bm) * B * H;
+  const int tiles = (L + 63) / 64;
+  const int64_t n_cu = cus > 0 ? cus : 1;
+  int splits = 1;
+  if (blocks > 0 && 4 * blocks <= n_cu) {
+    const int64_t fit = n_cu / blocks;
+    splits = static_cast<int>(fit < kMaxKeySplits ? fit : kMaxKeySplits);
+    if (splits > tiles / 2) splits = tiles / 2;
+    if (splits < 2) splits = 1;
+  }
+  const int st = (tiles + splits - 1) / splits;
+  if (split_tiles) *split_tiles = st;
+  return (tiles + st - 1) / st;
+}
+
+size_t rel_attention_workspace_bytes(int splits, int B, int H, int L, int D) {
+  if (splits <= 1) return 0;
+  return static_cast<size_t>(splits) * B * L * H * static_cast<size_t>(D + 2) * sizeof(float);
+}
 
 int launch_rel_attention_16bit(const RelParams& prm, int D, int dtype, hipStream_t stream) {
 #define DFLASH_REL_CASE(TYPE, DIM) \

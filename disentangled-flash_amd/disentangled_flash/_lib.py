@@ -18,7 +18,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load torch's HIP runtime first)
 
 LIBRARY_NAME = "libdflash.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_CODES = {
     torch.float16: 0,
@@ -59,6 +59,17 @@ def _bind(lib: ctypes.CDLL) -> None:
         _c_int, _c_int, _c_int, _c_int, _c_int,      # B, H, L, D, S
         _c_float, _c_int, _c_int, _c_int, _c_int,    # scale, has_c2p, has_p2c, dtype, strict
         _c_void_p,                                   # stream
+    ]
+    lib.dflash_attention_rel_split_plan.restype = _c_int
+    lib.dflash_attention_rel_split_plan.argtypes = [
+        _c_int, _c_int, _c_int, _c_int,                           # B, H, L, D
+        ctypes.POINTER(_c_int), ctypes.POINTER(ctypes.c_size_t),  # splits, workspace_bytes
+    ]
+    lib.dflash_attention_rel_fwd_split.restype = _c_int
+    lib.dflash_attention_rel_fwd_split.argtypes = [
+        *lib.dflash_attention_rel_fwd.argtypes[:-1],              # as dflash_attention_rel_fwd
+        _c_int, _c_void_p, ctypes.c_size_t,                       # splits, workspace, bytes
+        _c_void_p,                                                # stream
     ]
     lib.dflash_add_layernorm_fwd.restype = _c_int
     lib.dflash_add_layernorm_fwd.argtypes = [

@@ -20,6 +20,7 @@ traces through them the way the reference relies on ``triton_op``.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any, NamedTuple
 
 import torch
@@ -113,12 +114,17 @@ def deberta_attention_rel(
     has_c2p: bool,
     has_p2c: bool,
     strict_fp32: bool,
+    key_splits: int = 0,
 ) -> torch.Tensor:
     """Fused attention with in-kernel relative scores.
 
     ``qkv`` is the fused projection output ``[B, L, 3*H*d]`` (Q, K, V column
     blocks); ``pos_key/pos_query`` are ``[H, S, d]``.  When a mode is off its
     position tensor is never read.  Output ``[B, L, H*d]``.
+
+    ``key_splits``: 0 lets the library split the key range of every query block
+    over several workgroups when the unsplit grid would leave the GPU underfilled
+    (``dflash_attention_rel_split_plan``); 1 never splits; n > 1 forces n splits.
     """
 
     lib = _lib.load()
@@ -129,7 +135,12 @@ def deberta_attention_rel(
     base = qkv.data_ptr()
     esize = qkv.element_size()
     active = pos_key.size(1) if has_c2p else (pos_query.size(1) if has_p2c else 0)
-    code = lib.dflash_attention_rel_fwd(
+    splits, workspace_bytes = _split_plan(lib, qkv.device, batch, num_heads, length, head_dim,
+                                          key_splits)
+    workspace = None
+    if workspace_bytes:
+        workspace = torch.empty(workspace_bytes // 4, device=qkv.device, dtype=torch.float32)
+    code = lib.dflash_attention_rel_fwd_split(
         base,
         base + hd * esize,
         base + 2 * hd * esize,
@@ -151,16 +162,43 @@ def deberta_attention_rel(
         int(has_p2c),
         _lib.DTYPE_CODES[qkv.dtype],
         int(strict_fp32),
+        splits,
+        workspace.data_ptr() if workspace is not None else None,
+        workspace_bytes,
         _lib.current_stream_handle(qkv.device),
     )
-    _lib.check(code, "dflash_attention_rel_fwd")
+    _lib.check(code, "dflash_attention_rel_fwd_split")
     return out
+
+
+_SPLIT_PLANS: dict[tuple, tuple[int, int]] = {}
+
+
+def _split_plan(lib, device: torch.device, batch: int, heads: int, length: int, head_dim: int,
+                key_splits: int) -> tuple[int, int]:
+    """(splits, workspace bytes) for one launch; cached per device and shape."""
+
+    if batch == 0 or key_splits == 1:
+        return 1, 0
+    key = (device.index, batch, heads, length, head_dim, key_splits)
+    plan = _SPLIT_PLANS.get(key)
+    if plan is None:
+        splits = ctypes.c_int(max(0, key_splits))
+        size = ctypes.c_size_t(0)
+        with torch.cuda.device(device):
+            _lib.check(lib.dflash_attention_rel_split_plan(batch, heads, length, head_dim,
+                                                           ctypes.byref(splits),
+                                                           ctypes.byref(size)),
+                       "dflash_attention_rel_split_plan")
+        plan = (splits.value, size.value)
+        _SPLIT_PLANS[key] = plan
+    return plan
 
 
 @deberta_attention_rel.register_fake
 def _deberta_attention_rel_fake(qkv, pos_key, pos_query, delta_to_local, attention_mask,
                                 num_heads, head_dim, score_scale_log2, has_c2p, has_p2c,
-                                strict_fp32):
+                                strict_fp32, key_splits=0):
     batch, length, _ = qkv.shape
     return qkv.new_empty((batch, length, num_heads * head_dim))
 

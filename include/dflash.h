@@ -2,8 +2,9 @@
  * dflash.h - C ABI of the MI355X (gfx950) DeBERTa disentangled-attention library.
  *
  * Plain pointers and sizes only: every tensor argument is a device pointer to
- * memory the caller owns; the library allocates nothing and launches on the
- * HIP stream it is given (NULL = the default stream).  Calls are asynchronous
+ * memory the caller owns; the library allocates nothing (the split-key form
+ * takes a workspace from the caller) and launches on the HIP stream it is
+ * given (NULL = the default stream).  Calls are asynchronous
  * with respect to the host, like the kernel launch they replace.
  *
  * Return value: 0 on success, a negative DFLASH_ERR_* code for an argument
@@ -15,6 +16,7 @@
 #ifndef DFLASH_H_
 #define DFLASH_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -23,7 +25,7 @@ extern "C" {
 
 #define DFLASH_API __attribute__((visibility("default")))
 
-#define DFLASH_ABI_VERSION 3
+#define DFLASH_ABI_VERSION 4
 
 #define DFLASH_DTYPE_FP16 0
 #define DFLASH_DTYPE_BF16 1
@@ -36,6 +38,7 @@ extern "C" {
 #define DFLASH_ERR_DTYPE (-4)
 #define DFLASH_ERR_ALIGN (-5)
 #define DFLASH_ERR_TOO_LARGE (-6)
+#define DFLASH_ERR_WORKSPACE (-7)
 
 /* Activation codes of the ConvLayer tail (the module's conv_act). */
 #define DFLASH_ACT_GELU 0 /* exact erf form, Hugging Face ACT2FN["gelu"] */
@@ -96,6 +99,45 @@ DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, cons
                              void* out, int B, int H, int L, int D, int S,
                              float score_scale_log2, int has_c2p, int has_p2c, int dtype,
                              int strict_fp32, void* stream);
+
+/*
+ * Split-key plan for dflash_attention_rel_fwd_split on the current device.
+ *
+ * No counterpart in the reference, whose launch grid is always
+ * (cdiv(L, BM), B*H) (/root/reference/src/disentangled_flash/kernel.py:405-417).
+ * When that grid leaves most of the GPU idle (small batches: B=1, L=512, H=12
+ * gives 48 workgroups for 256 CUs), splitting the key range of every query
+ * block over `splits` workgroups and merging their partial rows fills it.  *splits on entry: 0 = choose for this shape and the current
+ * device, 1..8 = the caller's count.  On return *splits is the count the split
+ * form runs (1 = no split; fewer than requested when L has fewer key tiles)
+ * and *workspace_bytes the workspace it needs (0 for 1).
+ */
+DFLASH_API int dflash_attention_rel_split_plan(int B, int H, int L, int D, int* splits,
+                                               size_t* workspace_bytes);
+
+/*
+ * dflash_attention_rel_fwd with the key range of every query block split over
+ * `splits` workgroups (1..8; fewer are used when L has fewer key tiles).
+ * Same arguments, output and numerics contract; in addition:
+ *   splits          : the split count, normally from dflash_attention_rel_split_plan
+ *   workspace       : device memory of at least the plan's workspace_bytes for this
+ *                     split count, 16-byte aligned, owned by the caller; it holds the
+ *                     partial rows (fp32) between the kernel and the merge, both
+ *                     launched on `stream`.  Calls that share a workspace must not
+ *                     overlap.  May be NULL when splits <= 1.
+ * splits <= 1 and dtype fp32 run dflash_attention_rel_fwd unchanged.
+ * Returns DFLASH_ERR_WORKSPACE when workspace_bytes is too small.
+ */
+DFLASH_API int dflash_attention_rel_fwd_split(const void* query, const void* key,
+                                              const void* value, int64_t stride_b,
+                                              int64_t stride_h, int64_t stride_l,
+                                              const void* pos_key, const void* pos_query,
+                                              const int32_t* delta_to_local,
+                                              const uint8_t* attention_mask, void* out, int B,
+                                              int H, int L, int D, int S, float score_scale_log2,
+                                              int has_c2p, int has_p2c, int dtype,
+                                              int strict_fp32, int splits, void* workspace,
+                                              size_t workspace_bytes, void* stream);
 
 /*
  * Fused residual add + LayerNorm of an encoder layer output.

@@ -68,14 +68,14 @@ def _fused_qkv(q, k, v):
     return torch.cat(flat, dim=-1).contiguous()
 
 
-def _run_rel(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c):
+def _run_rel(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c, key_splits=0):
     from disentangled_flash.kernel import deberta_attention_rel
 
     d = q.shape[-1]
     factor = 1 + int(has_c2p) + int(has_p2c)
     scale_log2 = LOG2E / math.sqrt(d * factor)
     out = deberta_attention_rel(_fused_qkv(q, k, v), pos_key, pos_query, lut, mask,
-                                q.shape[1], d, scale_log2, has_c2p, has_p2c, True)
+                                q.shape[1], d, scale_log2, has_c2p, has_p2c, True, key_splits)
     torch.cuda.synchronize()
     return out
 
@@ -206,6 +206,63 @@ def test_rel_kernel_reads_strided_qkv_without_copies():
                                 LOG2E / math.sqrt(192), True, True, True)
     torch.cuda.synchronize()
     _check(out, *args, True, True, "strided")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 8])
+@pytest.mark.parametrize("pattern", ["right", "left", "holes", "boundary"])
+@pytest.mark.parametrize("dim,heads", [(32, 3), (64, 2), (128, 2)])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_rel_kernel_key_splits(splits, pattern, dim, heads, dtype):
+    """Split-key form (partial rows merged by a second kernel) against the oracle."""
+
+    args = _inputs(3, heads, 448, dim, DTYPES[dtype], pattern, seed=splits + dim)
+    for has_c2p, has_p2c in ((True, True), (True, False), (False, True)):
+        out = _run_rel(*args, has_c2p, has_p2c, key_splits=splits)
+        _check(out, *args, has_c2p, has_p2c, f"splits={splits} {pattern} d={dim}")
+
+
+def test_split_plan_fills_small_batches():
+    """B=1, L=512, H=12 (48 workgroups unsplit): the plan splits, and the result agrees
+    with the single-pass kernel and the oracle; B=32 is not split."""
+
+    import ctypes
+
+    from disentangled_flash import _lib
+
+    lib = _lib.load()
+    splits, size = ctypes.c_int(0), ctypes.c_size_t(0)
+    assert lib.dflash_attention_rel_split_plan(1, 12, 512, 64, ctypes.byref(splits),
+                                               ctypes.byref(size)) == 0
+    assert splits.value > 1 and size.value == splits.value * 512 * 12 * 66 * 4
+    big = ctypes.c_int(0)
+    assert lib.dflash_attention_rel_split_plan(32, 12, 512, 64, ctypes.byref(big),
+                                               ctypes.byref(size)) == 0
+    assert big.value == 1 and size.value == 0
+    args = _inputs(1, 12, 512, 64, torch.float16, "right", seed=21)
+    auto = _run_rel(*args, True, True)
+    single = _run_rel(*args, True, True, key_splits=1)
+    _check(auto, *args, True, True, "auto split")
+    assert (auto.float() - single.float()).abs().max().item() <= 2e-3
+
+
+def test_split_rejects_a_small_workspace():
+    from disentangled_flash import _lib
+
+    lib = _lib.load()
+    s, lut = _lut(256, "cuda")
+    qkv = torch.zeros(1, 256, 3 * 64, device="cuda", dtype=torch.float16)
+    pos = torch.zeros(1, s, 64, device="cuda", dtype=torch.float16)
+    mask = torch.ones(1, 256, device="cuda", dtype=torch.bool)
+    out = torch.empty(1, 256, 64, device="cuda", dtype=torch.float16)
+    ws = torch.empty(16, device="cuda", dtype=torch.float32)
+    base, e = qkv.data_ptr(), qkv.element_size()
+    args = [base, base + 64 * e, base + 128 * e, 256 * 192, 64, 192, pos.data_ptr(),
+            pos.data_ptr(), lut.data_ptr(), mask.data_ptr(), out.data_ptr(), 1, 1, 256, 64, s,
+            0.1, 1, 1, 0, 1]
+    assert lib.dflash_attention_rel_fwd_split(*args, 4, ws.data_ptr(), 64, None) == -7
+    assert lib.dflash_attention_rel_fwd_split(*args, 4, None, 0, None) == -1
+    assert lib.dflash_attention_rel_fwd_split(*args, 9, ws.data_ptr(), 64, None) == -2
+    assert b"workspace" in lib.dflash_error_string(-7)
 
 
 def test_c_abi_rejects_bad_arguments():
