@@ -172,7 +172,7 @@ struct RelLayout {
 
 }  // namespace
 
-template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C>
+template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C, bool SPLIT>
 __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
   using M = Mma<T>;
   using F = typename M::frag;
@@ -208,8 +208,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   const int L = p.L;
   const int mk = xcd_logical_block(blockIdx.x, gridDim.x);
-  const int split = mk % p.splits;  // key split (the splits of a block are neighbours)
-  const int m = mk / p.splits;
+  // Key split of the split-key form (the splits of a block are neighbours).
+  const int split = SPLIT ? mk % p.splits : 0;
+  const int m = SPLIT ? mk / p.splits : mk;
   const int bh = m / p.nqb;
   const int qblk = m - bh * p.nqb;
   const int b = bh / p.H;
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // masking like any other padded key.)  A padded query in range attends
   // uniformly to all L keys: its output is the mean of V over the sequence,
   // which does not depend on the query and is computed separately (v_mean below).
-  const int jstart = split * p.split_tiles * BN;  // 0 without splits
+  const int jstart = SPLIT ? split * p.split_tiles * BN : 0;
 
   // Mean of V over the L keys of (b, h) in fp32, left in LDS at vmean[0..D).
   float* vred = reinterpret_cast<float*>(smem);
@@ -495,7 +496,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   for (int qb = 0; qb < kQB; ++qb) qkept[qb] = qm[qb] != 0;
 
   if (!wg_kept) {
-    if (split > 0) return;  // split 0 stores the mean of V
+    if (SPLIT && split > 0) return;  // split 0 stores the mean of V
     // Every query of the workgroup is padded (or past L): all rows are the mean of V.
     v_mean();
     const int row_lo = i0 + tid / (D / 4);
@@ -573,7 +574,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   }
   // A kept query's own key is kept: klast >= 0 when wg_kept.
-  const int jend = p.splits > 1 ? min(klast + 1, jstart + p.split_tiles * BN) : klast + 1;
+  const int jend = SPLIT ? min(klast + 1, jstart + p.split_tiles * BN) : klast + 1;
 
   // ---- prologue: carried c2p chunks of tile 0 ----
   if constexpr (C2P) {
@@ -650,7 +651,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     lds_barrier();
     if constexpr (VBUFS == 1) {
       stage_v(Vt);
-      prefetch_v(jn);
+      prefetch_v(SPLIT && jn >= jend ? L : jn);
     }
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
@@ -743,8 +744,11 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     stage_k();
     if constexpr (VBUFS == 2) stage_v(Vt + (vbuf ^ 1) * LY::VT_SIZE);
     kept_next = __ballot(pmask != 0);
-    prefetch_k(jn + BN);
-    if constexpr (VBUFS == 2) prefetch_v(jn + BN);
+    // A split's tiles past its range are redirected past L: the buffer loads
+    // then return zeros without touching memory.
+    const int jpre = SPLIT && jn + BN >= jend ? L : jn + BN;
+    prefetch_k(jpre);
+    if constexpr (VBUFS == 2) prefetch_v(jpre);
     c2p_products();
 
     // ---- relative scores ----
@@ -893,7 +897,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       row_sum[qb] += __shfl_xor(row_sum[qb], 32);
     }
   }
-  if (p.splits > 1) {
+  if constexpr (SPLIT) {
     // Partial rows of this key split: unnormalised O, the exponent base and
     // the row sum (the merge kernel combines the splits of kept rows).  Split 0
     // also stores the padded rows, which do not depend on the keys.
@@ -1030,14 +1034,20 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   using LY = RelLayout<T, D, QW, BN, VB>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
-  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C>;
-  hipError_t err = ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
-  if (err != hipSuccess) return static_cast<int>(err);
+  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false>;
+  constexpr auto split_kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, true>;
   if (prm.splits < 1) prm.splits = 1;
+  hipError_t err = prm.splits > 1 ? ensure_dynamic_lds<split_kernel>(static_cast<int>(LY::bytes))
+                                  : ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
+  if (err != hipSuccess) return static_cast<int>(err);
   const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H * prm.splits;
   if (blocks > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), LY::bytes,
-                     stream, prm);
+  if (prm.splits > 1)
+    hipLaunchKernelGGL(split_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                       LY::bytes, stream, prm);
+  else
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), LY::bytes,
+                       stream, prm);
   err = hipGetLastError();
   if (err != hipSuccess || prm.splits == 1) return static_cast<int>(err);
   const int64_t rows = static_cast<int64_t>(prm.B) * prm.L * prm.H;
