@@ -260,9 +260,10 @@ def test_hip_graph_buckets_replay_eager_results():
     model = enable_deberta_inference(base.to("cuda", torch.float16), backend="hip",
                                      sequence_lengths=[64, 128, 512])
     encoder = model.encoder
-    # (32, 512) is the C3 shape, where hipBLASLt picks its stream-K kernels
-    buckets = capture_deberta_buckets(encoder, [(2, 64), (3, 128), (2, 64), (32, 512)])
-    assert sorted(buckets) == [(2, 64), (3, 128), (32, 512)]
+    # (32, 512) is the C3 shape, where hipBLASLt picks its stream-K kernels; (1, 512)
+    # runs the split-key attention (partial rows in a workspace from the graph's pool)
+    buckets = capture_deberta_buckets(encoder, [(2, 64), (3, 128), (2, 64), (32, 512), (1, 512)])
+    assert sorted(buckets) == [(1, 512), (2, 64), (3, 128), (32, 512)]
     with torch.inference_mode():
         for replay in range(3):
             for (batch, length), bucket in buckets.items():
