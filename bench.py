@@ -331,6 +331,39 @@ def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
     return rows
 
 
+def bench_mfma_ceiling():
+    """Practical fp16 MFMA ceiling: the probe kernel (csrc/probe/mfma_probe.hip) at 1, 2, 4
+    and 8 wavefronts per SIMD, each launch ~5 ms, after the clock ramp."""
+
+    import ctypes
+
+    from disentangled_flash import _lib
+
+    lib = ctypes.CDLL(str(_lib.library_path().with_name("libdflash_probe.so")))
+    lib.dflash_probe_mfma.restype = ctypes.c_int
+    lib.dflash_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    src = torch.randn(4096 * 8, device="cuda", dtype=torch.float16)
+    rows = []
+    for waves in (1, 2, 4, 8):
+        blocks = cus * waves
+        iters = max(1, 70000 // waves)
+        dst = torch.empty(blocks * 256, device="cuda", dtype=torch.float32)
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def run():
+            code = lib.dflash_probe_mfma(src.data_ptr(), dst.data_ptr(), blocks, iters, stream)
+            if code != 0:
+                raise RuntimeError(f"mfma probe launch failed ({code})")
+
+        ms = time_launches(run, 5, 2)
+        flops = blocks * 4 * iters * 8 * 16 * 16 * 32 * 2
+        rows.append({"waves_per_simd": waves, "ms": round(ms, 3),
+                     "tflops": round(flops / (ms * 1e-3) / 1e12, 1)})
+    return rows
+
+
 def bench_edge(steps: int, warmup: int):
     """C5 edge sweep: the fused attention op for d=128/H=8 (B=16, L=512) and d=32/H=16
     (B=16, L=384) in fp16/bf16/fp32 x {c2p, p2c, c2p|p2c}, boundary valid lengths
@@ -481,6 +514,8 @@ def main() -> int:
                         help="C4 24-layer xlarge bf16 encoder per bucket, one JSON line")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="one 256 MiB device-to-device copy (HBM counter calibration)")
+    parser.add_argument("--mfma-ceiling", action="store_true",
+                        help="fp16 MFMA-only throughput at 1/2/4/8 wavefronts per SIMD")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
@@ -522,6 +557,10 @@ def main() -> int:
     if args.encoder_only:
         enc = bench_encoder(32, 512, args.encoder_steps, 3, backends=("hip",))
         log(f"encoder: {enc}")
+        return 0
+    if args.mfma_ceiling:
+        print(json.dumps({"mfma_ceiling": "v_mfma_f32_16x16x32_f16 only, TFLOP/s",
+                          "rows": bench_mfma_ceiling()}), flush=True)
         return 0
     if args.kernel_only:
         inp = c2_inputs(torch.float16, padded=False)

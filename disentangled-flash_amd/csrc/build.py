@@ -23,6 +23,10 @@ PACKAGE_ROOT = CSRC.parent
 REPO_ROOT = PACKAGE_ROOT.parent
 INCLUDE = REPO_ROOT / "include"
 OUTPUT = PACKAGE_ROOT / "disentangled_flash" / "libdflash.so"
+# Measurement probes (bench.py --mfma-ceiling), a library of their own so that
+# libdflash exports only the C ABI of include/dflash.h.
+PROBE_SOURCES = CSRC / "probe"
+PROBE_OUTPUT = PACKAGE_ROOT / "disentangled_flash" / "libdflash_probe.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU instructions.
@@ -61,7 +65,13 @@ def _run(command: list[str], verbose: bool) -> None:
 
 
 def build(jobs: int | None = None, verbose: bool = False, output: Path = OUTPUT) -> Path:
-    sources = sorted(CSRC.glob("*.hip"))
+    _build_library(sorted(CSRC.glob("*.hip")), output, jobs, verbose)
+    if output == OUTPUT:
+        _build_library(sorted(PROBE_SOURCES.glob("*.hip")), PROBE_OUTPUT, jobs, verbose)
+    return output
+
+
+def _build_library(sources: list[Path], output: Path, jobs: int | None, verbose: bool) -> None:
     if not sources:
         raise RuntimeError(f"no HIP sources in {CSRC}")
     compiler = hipcc()
@@ -83,7 +93,6 @@ def build(jobs: int | None = None, verbose: bool = False, output: Path = OUTPUT)
         )
         output.parent.mkdir(parents=True, exist_ok=True)
         shutil.move(str(staged), str(output))
-    return output
 
 
 def main() -> None:
@@ -92,7 +101,7 @@ def main() -> None:
     parser.add_argument("--verbose", action="store_true")
     args = parser.parse_args()
     path = build(jobs=args.jobs, verbose=args.verbose)
-    print(f"built {path}")
+    print(f"built {path} and {PROBE_OUTPUT.name}")
 
 
 if __name__ == "__main__":
