@@ -331,7 +331,7 @@ def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
     return rows
 
 
-def bench_mfma_ceiling():
+def bench_mfma_ceiling(wave_counts=(1, 2, 4, 8)):
     """Practical fp16 MFMA ceiling: the probe kernel (csrc/probe/mfma_probe.hip) at 1, 2, 4
     and 8 wavefronts per SIMD, each launch ~5 ms, after the clock ramp."""
 
@@ -346,7 +346,7 @@ def bench_mfma_ceiling():
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     src = torch.randn(4096 * 8, device="cuda", dtype=torch.float16)
     rows = []
-    for waves in (1, 2, 4, 8):
+    for waves in wave_counts:
         blocks = cus * waves
         iters = max(1, 70000 // waves)
         dst = torch.empty(blocks * 256, device="cuda", dtype=torch.float32)
@@ -640,6 +640,12 @@ def main() -> int:
     }
     del full
     torch.cuda.empty_cache()
+    # The fp16 MFMA rate an MFMA-only stream sustains at the kernel's occupancy
+    # (two wavefronts per SIMD), beside the spec peak.
+    practical = bench_mfma_ceiling((2,))[0]["tflops"]
+    line["roofline"]["practical_peak_2_waves_per_simd"] = practical
+    line["roofline"]["f_total_practical_frac"] = round(line["roofline"]["f_total_tflops"] / practical, 4)
+    log(f"MFMA-only stream at two wavefronts per SIMD: {practical} TFLOP/s")
 
     if not args.skip_encoder:
         enc = bench_encoder(32, 512, args.encoder_steps, 3)
