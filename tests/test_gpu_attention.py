@@ -325,3 +325,23 @@ def test_rel_kernel_long_sequences(length, dtype):
     args = _inputs(1, 2, length, 64, DTYPES[dtype], "right", seed=length + 1)
     out = _run_rel(*args, True, True)
     _check(out, *args, True, True, f"L={length}")
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_rel_kernel_random_shapes(case):
+    """Seeded random shapes, masks, modes and key splits against the oracle."""
+
+    rng = torch.Generator().manual_seed(1000 + case)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]  # noqa: E731
+    dim, heads = pick([(32, 3), (64, 2), (128, 1)])
+    length = int(torch.randint(1, 700, (1,), generator=rng))
+    batch = int(torch.randint(1, 4, (1,), generator=rng))
+    dtype = pick(["fp16", "bf16"])
+    pattern = pick(["right", "left", "holes", "boundary", "none"])
+    has_c2p, has_p2c = pick([(True, True), (True, False), (False, True)])
+    splits = pick([0, 1, 2, 5])
+    args = _inputs(batch, heads, length, dim, DTYPES[dtype], pattern, seed=case)
+    out = _run_rel(*args, has_c2p, has_p2c, key_splits=splits)
+    _check(out, *args, has_c2p, has_p2c,
+           f"case {case}: B={batch} H={heads} L={length} d={dim} {dtype} {pattern} "
+           f"c2p={has_c2p} p2c={has_p2c} splits={splits}")
