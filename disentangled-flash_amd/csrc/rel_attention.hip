@@ -752,24 +752,43 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     c2p_products();
 
     // ---- relative scores ----
-    if constexpr (C2P || P2C) {
+    if constexpr (C2P && P2C) {
+      // All 32 reads of a query block first, then the adds: written element by
+      // element, the compiler interleaved read, wait and add and left most of
+      // the LDS latency exposed.
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb)
+      for (int qb = 0; qb < kQB; ++qb) {
+        T cvs[KB][4], pvs[KB][4];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int off = 16 * (qb - kb) - 4 * r - kMinOff;
-            if constexpr (C2P && P2C) {
-              const T cv = cw_lane[16 * qb * LY::CW_LD + off];
-              const T pv2 = pw_lane[(16 * kb + 4 * r) * LY::PW_LD + off];
-              sc[kb][qb][r] = add2<T>(sc[kb][qb][r], cv, pv2);
-            } else if constexpr (C2P) {
-              sc[kb][qb][r] += static_cast<float>(cw_lane[16 * qb * LY::CW_LD + off]);
-            } else {
-              sc[kb][qb][r] += static_cast<float>(pw_lane[(16 * kb + 4 * r) * LY::PW_LD + off]);
-            }
+            cvs[kb][r] = cw_lane[16 * qb * LY::CW_LD + off];
+            pvs[kb][r] = pw_lane[(16 * kb + 4 * r) * LY::PW_LD + off];
           }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[kb][qb][r] = add2<T>(sc[kb][qb][r], cvs[kb][r], pvs[kb][r]);
+      }
+    } else if constexpr (C2P || P2C) {
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) {
+        T vals[KB][4];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int off = 16 * (qb - kb) - 4 * r - kMinOff;
+            vals[kb][r] = C2P ? cw_lane[16 * qb * LY::CW_LD + off]
+                              : pw_lane[(16 * kb + 4 * r) * LY::PW_LD + off];
+          }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[kb][qb][r] += static_cast<float>(vals[kb][r]);
+      }
     }
 
     // ---- masking (wavefront-uniform slow path: tiles with a padded key or past L) ----
