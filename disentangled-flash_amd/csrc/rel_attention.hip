@@ -662,12 +662,22 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     // runtime skips (below): with four copies it runs out of registers.
     auto qk_p2c = [&](auto wave_c) {
       constexpr int W = decltype(wave_c)::value;
+      // K fragments one key block ahead (two register sets), so that the
+      // reads of block kb + 1 are in flight during the MFMAs of block kb.
+      F kfa[2][KD];
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd)
+        kfa[0][kd] = *reinterpret_cast<const F*>(Ks + key_of(c) * LY::KS_LD + 32 * kd + 8 * g);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         F kf[KD];
 #pragma unroll
-        for (int kd = 0; kd < KD; ++kd)
-          kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+        for (int kd = 0; kd < KD; ++kd) kf[kd] = kfa[kb & 1][kd];
+        if (kb + 1 < KB) {
+#pragma unroll
+          for (int kd = 0; kd < KD; ++kd)
+            kfa[(kb + 1) & 1][kd] = *reinterpret_cast<const F*>(Ks + (16 * (kb + 1) + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+        }
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
           f32x4_t acc{0.f, 0.f, 0.f, 0.f};
