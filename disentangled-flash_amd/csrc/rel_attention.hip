@@ -824,6 +824,33 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
     }
 
+    // PV operands (V^T through transposing reads).  For d = 128 all of them are
+    // read before the softmax so that their LDS latency hides under it (93.9 ->
+    // 88.6 us on the C5 shape); for d <= 64 that cost more registers than it
+    // saved (+2 %), and they are read next to their MFMAs.
+    auto vt_frag = [&](int ks, int db) {
+      // Lane c of group g supplies row 32ks + 4(c>>2) + g (+16 for the upper
+      // half), columns 16db + 4(c&3) .. +3, and receives V[rows of its
+      // k-slice][16db + c] -- keys g + 4e and 16 + g + 4e, the order of the P^T
+      // operand.  The result is moved as whole dwords: assembling the operand
+      // from its 16-bit elements was compiled into wrong code.
+      const T* p_lo = vt_cur + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
+      const T* p_hi = p_lo + 16 * LY::VS_LD;
+      const u32x2_t lo = __builtin_bit_cast(
+          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
+      const u32x2_t hi = __builtin_bit_cast(
+          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
+      return __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+    };
+    constexpr bool kVtEarly = D >= 128 && !SPLIT;
+    F vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
+    if constexpr (kVtEarly) {
+#pragma unroll
+      for (int ks = 0; ks < BN / 32; ++ks)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) vt_all[ks][db] = vt_frag(ks, db);
+    }
+
     // ---- online softmax (exp2, stale maximum) ----
     // The exponent base only has to be common to a row and keep exp2 finite,
     // so the previous maximum is reused while no scaled score exceeds it by
@@ -891,19 +918,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        // Transposing reads: lane c of group g supplies row 32ks + 4(c>>2) + g
-        // (+16 for the upper half), columns 16db + 4(c&3) .. +3, and receives
-        // V[rows of its k-slice][16db + c] -- keys g + 4e and 16 + g + 4e,
-        // the order of the P^T operand.
-        const T* p_lo = vt_cur + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
-        const T* p_hi = p_lo + 16 * LY::VS_LD;
-        // (The result is moved as whole dwords: assembling the operand from its
-        // 16-bit elements was compiled into wrong code.)
-        const u32x2_t lo = __builtin_bit_cast(
-            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
-        const u32x2_t hi = __builtin_bit_cast(
-            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
-        const F a = __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+        F a;
+        if constexpr (kVtEarly) {
+          a = vt_all[ks][db];
+        } else {
+          a = vt_frag(ks, db);
+        }
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
       }
@@ -1108,7 +1128,9 @@ int rel_attention_splits(int B, int H, int L, int D, int cus, int* split_tiles) 
   const int tiles = (L + 63) / 64;
   const int64_t n_cu = cus > 0 ? cus : 1;
   int splits = 1;
-  if (blocks > 0 && 4 * blocks <= n_cu) {
+  // d = 128: the split instance runs out of registers (272 B of spills) and is
+  // slower than the unsplit kernel even at B = 1 (29.3 against 26.9 us).
+  if (D <= 64 && blocks > 0 && 4 * blocks <= n_cu) {
     const int64_t fit = n_cu / blocks;
     splits = static_cast<int>(fit < kMaxKeySplits ? fit : kMaxKeySplits);
     if (splits > tiles / 2) splits = tiles / 2;
