@@ -824,10 +824,11 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
     }
 
-    // PV operands (V^T through transposing reads).  For d = 128 all of them are
-    // read before the softmax so that their LDS latency hides under it (93.9 ->
-    // 88.6 us on the C5 shape); for d <= 64 that cost more registers than it
-    // saved (+2 %), and they are read next to their MFMAs.
+    // PV operands (V^T through transposing reads).  For d = 128 with both
+    // relative terms all of them are read before the softmax so that their LDS
+    // latency hides under it (93.9 -> 89.3 us on the C5 shape); with one term,
+    // or for d <= 64, that cost more registers than it saved (+2-5 %), and they
+    // are read next to their MFMAs.
     auto vt_frag = [&](int ks, int db) {
       // Lane c of group g supplies row 32ks + 4(c>>2) + g (+16 for the upper
       // half), columns 16db + 4(c&3) .. +3, and receives V[rows of its
@@ -842,7 +843,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
       return __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
     };
-    constexpr bool kVtEarly = D >= 128 && !SPLIT;
+    constexpr bool kVtEarly = D >= 128 && !SPLIT && C2P && P2C;
     F vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
     if constexpr (kVtEarly) {
 #pragma unroll
