@@ -127,6 +127,8 @@ def deberta_attention_rel(
     (``dflash_attention_rel_split_plan``); 1 never splits; n > 1 forces n splits.
     """
 
+    if key_splits < 0:
+        raise ValueError(f"key_splits must be >= 0, got {key_splits}")
     lib = _lib.load()
     batch, length, width = qkv.shape
     hd = num_heads * head_dim
@@ -183,7 +185,7 @@ def _split_plan(lib, device: torch.device, batch: int, heads: int, length: int, 
     key = (device.index, batch, heads, length, head_dim, key_splits)
     plan = _SPLIT_PLANS.get(key)
     if plan is None:
-        splits = ctypes.c_int(max(0, key_splits))
+        splits = ctypes.c_int(key_splits)
         size = ctypes.c_size_t(0)
         with torch.cuda.device(device):
             _lib.check(lib.dflash_attention_rel_split_plan(batch, heads, length, head_dim,

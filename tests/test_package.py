@@ -170,6 +170,14 @@ def test_hip_module_validation_errors_on_cpu():
         _require_2d_padding_mask(torch.ones(1, 1, 4, 4), 1, 4)
     with pytest.raises(ValueError, match="does not match"):
         _require_2d_padding_mask(torch.ones(2, 4), 1, 4)
+    from disentangled_flash.kernel import deberta_attention_rel
+
+    qkv = torch.zeros(1, 4, 3 * 64, dtype=torch.float16)
+    rows = torch.zeros(2, 7, 32, dtype=torch.float16)
+    with pytest.raises(ValueError, match="key_splits"):
+        deberta_attention_rel(qkv, rows, rows, torch.zeros(7, dtype=torch.int32),
+                              torch.ones(1, 4, dtype=torch.uint8), 2, 32, 1.0, True, True,
+                              False, key_splits=-1)
 
 
 def _tiny_deberta(layers=2, conv=3):
