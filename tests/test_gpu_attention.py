@@ -187,6 +187,33 @@ def test_c2_full_size(dtype, pattern):
     assert (table.double() - ref).abs().max().item() <= TOL[DTYPES[dtype]]
 
 
+def test_c2_deterministic_and_batch_invariant():
+    """Bit-exact properties at the C2 shape: two launches agree, and a sequence's
+    output does not depend on the rest of the batch (each workgroup reads only its
+    own sequence), also in the split-key form."""
+
+    gen = torch.Generator().manual_seed(77)
+    b, h, length, d = 32, 12, 512, 64
+    s, lut = _lut(length, "cuda")
+    scale = 1.0 / math.sqrt(d)
+    q, k, v = (torch.randn(b, h, length, d, generator=gen) * scale for _ in range(3))
+    pos_key, pos_query = (torch.randn(h, s, d, generator=gen) * scale for _ in range(2))
+    lengths = torch.randint(1, 513, (b,), generator=gen)
+    mask = (torch.arange(length)[None] < lengths[:, None]).cuda()
+    q, k, v, pos_key, pos_query = (t.to("cuda", torch.float16) for t in (q, k, v, pos_key, pos_query))
+    first = _run_rel(q, k, v, pos_key, pos_query, lut, mask, True, True, key_splits=1)
+    again = _run_rel(q, k, v, pos_key, pos_query, lut, mask, True, True, key_splits=1)
+    assert torch.equal(first, again)
+    for i in (0, 17, 31):
+        one = [t[i:i + 1] for t in (q, k, v)]
+        alone = _run_rel(*one, pos_key, pos_query, lut, mask[i:i + 1], True, True, key_splits=1)
+        assert torch.equal(alone[0], first[i]), f"sequence {i} (length {int(lengths[i])})"
+        split_a = _run_rel(*one, pos_key, pos_query, lut, mask[i:i + 1], True, True, key_splits=4)
+        split_b = _run_rel(*one, pos_key, pos_query, lut, mask[i:i + 1], True, True, key_splits=4)
+        assert torch.equal(split_a, split_b)
+        assert (split_a.float() - first[i:i + 1].float()).abs().max().item() <= 2e-3
+
+
 def test_rel_and_table_agree_fp32():
     args = _inputs(2, 3, 257, 64, torch.float32, "right", seed=9)
     a = _run_rel(*args, True, True)
