@@ -598,15 +598,28 @@ int dispatch_modes(const Params& prm, int has_c2p, int has_p2c, hipStream_t stre
   return launch<T, D, false, false, TABLE>(prm, stream);
 }
 
+// Table mode serves every dtype; the windowed form of this kernel serves fp32
+// only (16-bit inputs run the relative-window kernel), so only its fp32
+// instances are compiled.
 template <bool TABLE>
 int dispatch(const Params& prm, int D, int dtype, int has_c2p, int has_p2c, hipStream_t stream) {
 #define DFLASH_CASE(TYPE, DIM)                                                     \
   if (D == DIM) return dispatch_modes<TYPE, DIM, TABLE>(prm, has_c2p, has_p2c, stream);
   switch (dtype) {
     case DFLASH_DTYPE_FP16:
-      DFLASH_CASE(_Float16, 32) DFLASH_CASE(_Float16, 64) DFLASH_CASE(_Float16, 128) break;
+      if constexpr (TABLE) {
+        DFLASH_CASE(_Float16, 32) DFLASH_CASE(_Float16, 64) DFLASH_CASE(_Float16, 128)
+      } else {
+        return DFLASH_ERR_DTYPE;
+      }
+      break;
     case DFLASH_DTYPE_BF16:
-      DFLASH_CASE(__bf16, 32) DFLASH_CASE(__bf16, 64) DFLASH_CASE(__bf16, 128) break;
+      if constexpr (TABLE) {
+        DFLASH_CASE(__bf16, 32) DFLASH_CASE(__bf16, 64) DFLASH_CASE(__bf16, 128)
+      } else {
+        return DFLASH_ERR_DTYPE;
+      }
+      break;
     case DFLASH_DTYPE_FP32:
       DFLASH_CASE(float, 32) DFLASH_CASE(float, 64) DFLASH_CASE(float, 128) break;
     default:
