@@ -538,10 +538,11 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   }
   prefetch_k(jstart);
   prefetch_v(jstart);
-  // Tile 1 (d <= 64; d = 128 has no registers to spare here): K/V and the
-  // rows of its new c2p chunks (lookups in lutc), moved into the pipeline
-  // registers once tile 0 has been staged and multiplied.
-  constexpr bool kEarlyTile1 = D <= 64;
+  // Tile 1 (d = 64 only: d = 128 has no registers to spare here, and d = 32,
+  // whose tiles are short, measured faster without it): K/V and the rows of
+  // its new c2p chunks (lookups in lutc), moved into the pipeline registers
+  // once tile 0 has been staged and multiplied.
+  constexpr bool kEarlyTile1 = D == 64;
   u32x4_t pk1[NCH];
   u32x4_t pv1[NVB];
   uint8_t pmask1 = 0;
