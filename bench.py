@@ -331,39 +331,6 @@ def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
     return rows
 
 
-def bench_mfma_ceiling(wave_counts=(1, 2, 4, 8)):
-    """Practical fp16 MFMA ceiling: the probe kernel (csrc/probe/mfma_probe.hip) at 1, 2, 4
-    and 8 wavefronts per SIMD, each launch ~5 ms, after the clock ramp."""
-
-    import ctypes
-
-    from disentangled_flash import _lib
-
-    lib = ctypes.CDLL(str(_lib.library_path().with_name("libdflash_probe.so")))
-    lib.dflash_probe_mfma.restype = ctypes.c_int
-    lib.dflash_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
-                                      ctypes.c_int, ctypes.c_void_p]
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    src = torch.randn(4096 * 8, device="cuda", dtype=torch.float16)
-    rows = []
-    for waves in wave_counts:
-        blocks = cus * waves
-        iters = max(1, 70000 // waves)
-        dst = torch.empty(blocks * 256, device="cuda", dtype=torch.float32)
-        stream = torch.cuda.current_stream().cuda_stream
-
-        def run():
-            code = lib.dflash_probe_mfma(src.data_ptr(), dst.data_ptr(), blocks, iters, stream)
-            if code != 0:
-                raise RuntimeError(f"mfma probe launch failed ({code})")
-
-        ms = time_launches(run, 5, 2)
-        flops = blocks * 4 * iters * 8 * 16 * 16 * 32 * 2
-        rows.append({"waves_per_simd": waves, "ms": round(ms, 3),
-                     "tflops": round(flops / (ms * 1e-3) / 1e12, 1)})
-    return rows
-
-
 def bench_edge(steps: int, warmup: int):
     """C5 edge sweep: the fused attention op for d=128/H=8 (B=16, L=512) and d=32/H=16
     (B=16, L=384) in fp16/bf16/fp32 x {c2p, p2c, c2p|p2c}, boundary valid lengths
@@ -452,44 +419,73 @@ def bench_c4(steps: int, warmup: int):
     return rows
 
 
-def cpu_baseline(target_seconds: float = 12.0):
+def cpu_baseline(target_seconds: float = 12.0, c1_seconds: float = 4.0):
     """Oracle restatement of the ``optimized`` equation, fp32, on the host CPU.
 
-    Bounded sample of the C2 workload: one sequence (B=1 of 32) at L=512, H=12,
-    d=64 per call, repeated for about ``target_seconds``; reported in the same
-    unit (F_attn TFLOP/s).
+    C2 (the reported value): a bounded sample of the C2 workload, one sequence
+    (B=1 of 32) at L=512, H=12, d=64 per call, repeated for about
+    ``target_seconds``, in the headline unit (F_attn TFLOP/s).  C1: the
+    CPU-runnable single layer (B=2, L=128, hidden 768, fused QKV projection
+    included), median milliseconds per call.
+
+    Threads: every host CPU, capped at the 16 a one-GPU box grants a job; both
+    the thread count and the host's CPU count are reported.
     """
 
-    from oracle.optimized import optimized_core
+    from oracle.optimized import optimized_attention, optimized_core
     from oracle.positions import compact_plan, dense_map
 
-    cores = min(os.cpu_count() or 1, 16)
+    host_cpus = os.cpu_count() or 1
+    cores = min(host_cpus, 16)
     torch.set_num_threads(cores)
+
+    def timed(fn, seconds):
+        for _ in range(2):
+            fn()
+        samples = []
+        start = time.perf_counter()
+        while time.perf_counter() - start < seconds or len(samples) < 5:
+            t0 = time.perf_counter()
+            fn()
+            samples.append(time.perf_counter() - t0)
+        return statistics.median(samples), len(samples), sum(samples)
+
+    def pair_map(length):
+        lut = compact_plan(length, position_buckets=256, max_relative_positions=512,
+                           position_embedding_size=256)[1]
+        return torch.from_numpy(dense_map(lut, length))
+
     inp = c2_inputs(torch.float32, padded=True, batch=1, device="cpu")
-    pair = torch.from_numpy(dense_map(compact_plan(512, position_buckets=256,
-                                                   max_relative_positions=512,
-                                                   position_embedding_size=256)[1], 512))
+    pair = pair_map(512)
     args = (inp["q"], inp["k"], inp["v"], inp["pos_key"], inp["pos_query"], pair, inp["mask"],
             math.sqrt(192))
-    for _ in range(2):
-        optimized_core(*args)
-    calls = 0
-    start = time.perf_counter()
-    samples = []
-    while time.perf_counter() - start < target_seconds:
-        t0 = time.perf_counter()
-        optimized_core(*args)
-        samples.append(time.perf_counter() - t0)
-        calls += 1
-    median = statistics.median(samples)
+    median, calls, total = timed(lambda: optimized_core(*args), target_seconds)
+
+    # C1: B=2, L=128, hidden 768, 12 heads, weights N(0, 0.02), lengths U[64, 128].
+    gen = torch.Generator().manual_seed(17)
+    hidden = torch.randn(2, 128, 768, generator=gen)
+    weight = torch.randn(3 * 768, 768, generator=gen) * 0.02
+    bias = torch.zeros(3 * 768)
+    s1 = compact_plan(128, position_buckets=256, max_relative_positions=512,
+                      position_embedding_size=256)[0].size
+    pk, pq = (torch.randn(12, s1, 64, generator=gen) * 0.02 for _ in range(2))
+    lengths = torch.randint(64, 129, (2,), generator=gen)
+    mask1 = torch.arange(128)[None] < lengths[:, None]
+    pair1 = pair_map(128)
+    c1_median, c1_calls, _ = timed(
+        lambda: optimized_attention(hidden, weight, bias, pk, pq, pair1, mask1, 12, 64), c1_seconds)
     return {
         "value": attention_flops(inp) / median / 1e12,
         "unit": "TFLOP/s",
         "cores": cores,
+        "host_cpus": host_cpus,
         "kind": "port",
-        "sample": (f"oracle/optimized.py optimized_core, fp32, B=1 of the B=32 C2 batch "
-                   f"(L=512 H=12 d=64, padded), {calls} calls in {sum(samples):.1f}s, "
-                   f"median {median * 1e3:.1f} ms/call"),
+        "sample": (f"oracle/optimized.py optimized_core, fp32, {cores} threads of {host_cpus} "
+                   f"host CPUs, B=1 of the B=32 C2 batch (L=512 H=12 d=64, padded), {calls} "
+                   f"calls in {total:.1f}s, median {median * 1e3:.2f} ms/call"),
+        "c1_layer_ms": round(c1_median * 1e3, 3),
+        "c1_sample": (f"oracle/optimized.py optimized_attention (fused QKV linear + attention), "
+                      f"fp32, C1 B=2 L=128 hidden 768 H=12, {c1_calls} calls, median"),
     }
 
 
@@ -514,8 +510,6 @@ def main() -> int:
                         help="C4 24-layer xlarge bf16 encoder per bucket, one JSON line")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="one 256 MiB device-to-device copy (HBM counter calibration)")
-    parser.add_argument("--mfma-ceiling", action="store_true",
-                        help="fp16 MFMA-only throughput at 1/2/4/8 wavefronts per SIMD")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures the single-GPU hot path only: this build runs on one GPU "
@@ -557,10 +551,6 @@ def main() -> int:
     if args.encoder_only:
         enc = bench_encoder(32, 512, args.encoder_steps, 3, backends=("hip",))
         log(f"encoder: {enc}")
-        return 0
-    if args.mfma_ceiling:
-        print(json.dumps({"mfma_ceiling": "v_mfma_f32_16x16x32_f16 only, TFLOP/s",
-                          "rows": bench_mfma_ceiling()}), flush=True)
         return 0
     if args.kernel_only:
         inp = c2_inputs(torch.float16, padded=False)
@@ -640,12 +630,6 @@ def main() -> int:
     }
     del full
     torch.cuda.empty_cache()
-    # The fp16 MFMA rate an MFMA-only stream sustains at the kernel's occupancy
-    # (two wavefronts per SIMD), beside the spec peak.
-    practical = bench_mfma_ceiling((2,))[0]["tflops"]
-    line["roofline"]["practical_peak_2_waves_per_simd"] = practical
-    line["roofline"]["f_total_practical_frac"] = round(line["roofline"]["f_total_tflops"] / practical, 4)
-    log(f"MFMA-only stream at two wavefronts per SIMD: {practical} TFLOP/s")
 
     if not args.skip_encoder:
         enc = bench_encoder(32, 512, args.encoder_steps, 3)

@@ -203,10 +203,14 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
       // Every delta of the tile has its own slot (inside the un-bucketed band,
       // no clamping): the local slot is the window index itself.
       identity = w_p == kBlockM + BN - 1 && dlo >= -(L - 1) && dhi <= L - 1;
-      // A plan whose lookup table steps by more than one slot per delta breaks
-      // the window precondition; clamp so LDS writes stay inside the buffers.
-      w_p = min(w_p, LY::WP_MAX);
-      w_c = min(w_c, LY::WC_MAX);
+      // A plan whose lookup table is not non-decreasing with steps of 0 or 1
+      // breaks the window precondition (its output is then undefined); clamp
+      // the widths to [0, MAX] so LDS writes stay inside the buffers and the
+      // row indices below stay inside [0, S).
+      w_p = max(0, min(w_p, LY::WP_MAX));
+      w_c = max(0, min(w_c, LY::WC_MAX));
+      lo_p = max(0, min(lo_p, S - 1));
+      lo_c = max(0, min(lo_c, S - 1));
     }
     const int nsc_p = (w_p + 15) >> 4;
     const int nsc_c = (w_c + 15) >> 4;
@@ -267,7 +271,10 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
 #pragma unroll
       for (int n = 0; n < NLW; ++n) {
         const int t = tid + n * kThreads;
-        if (t < kBlockM + BN - 1) Lw[t] = plut[n] - lo_p;
+        // Windowed: local slots relative to the window start, clamped into the
+        // window (only a plan breaking the step precondition needs the clamp).
+        if (t < kBlockM + BN - 1)
+          Lw[t] = WINDOWED ? max(0, min(plut[n] - lo_p, LY::WP_MAX - 1)) : plut[n];
       }
     }
     lds_barrier();

@@ -23,10 +23,6 @@ PACKAGE_ROOT = CSRC.parent
 REPO_ROOT = PACKAGE_ROOT.parent
 INCLUDE = REPO_ROOT / "include"
 OUTPUT = PACKAGE_ROOT / "disentangled_flash" / "libdflash.so"
-# Measurement probes (bench.py --mfma-ceiling), a library of their own so that
-# libdflash exports only the C ABI of include/dflash.h.
-PROBE_SOURCES = CSRC / "probe"
-PROBE_OUTPUT = PACKAGE_ROOT / "disentangled_flash" / "libdflash_probe.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting packed fp32 VALU instructions.
@@ -66,8 +62,6 @@ def _run(command: list[str], verbose: bool) -> None:
 
 def build(jobs: int | None = None, verbose: bool = False, output: Path = OUTPUT) -> Path:
     _build_library(sorted(CSRC.glob("*.hip")), output, jobs, verbose)
-    if output == OUTPUT:
-        _build_library(sorted(PROBE_SOURCES.glob("*.hip")), PROBE_OUTPUT, jobs, verbose)
     return output
 
 
@@ -101,7 +95,7 @@ def main() -> None:
     parser.add_argument("--verbose", action="store_true")
     args = parser.parse_args()
     path = build(jobs=args.jobs, verbose=args.verbose)
-    print(f"built {path} and {PROBE_OUTPUT.name}")
+    print(f"built {path}")
 
 
 if __name__ == "__main__":

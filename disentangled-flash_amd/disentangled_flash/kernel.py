@@ -129,6 +129,8 @@ def deberta_attention_rel(
 
     if key_splits < 0:
         raise ValueError(f"key_splits must be >= 0, got {key_splits}")
+    _check_rel_inputs(qkv, pos_key, pos_query, delta_to_local, attention_mask, num_heads,
+                      head_dim, has_c2p, has_p2c)
     lib = _lib.load()
     batch, length, width = qkv.shape
     hd = num_heads * head_dim
@@ -137,8 +139,8 @@ def deberta_attention_rel(
     base = qkv.data_ptr()
     esize = qkv.element_size()
     active = pos_key.size(1) if has_c2p else (pos_query.size(1) if has_p2c else 0)
-    splits, workspace_bytes = _split_plan(lib, qkv.device, batch, num_heads, length, head_dim,
-                                          key_splits)
+    splits, workspace_bytes = _split_plan(lib, qkv.device, qkv.dtype, batch, num_heads, length,
+                                          head_dim, key_splits)
     workspace = None
     if workspace_bytes:
         workspace = torch.empty(workspace_bytes // 4, device=qkv.device, dtype=torch.float32)
@@ -176,11 +178,64 @@ def deberta_attention_rel(
 _SPLIT_PLANS: dict[tuple, tuple[int, int]] = {}
 
 
-def _split_plan(lib, device: torch.device, batch: int, heads: int, length: int, head_dim: int,
-                key_splits: int) -> tuple[int, int]:
-    """(splits, workspace bytes) for one launch; cached per device and shape."""
+def _check_rel_inputs(qkv, pos_key, pos_query, delta_to_local, attention_mask, num_heads,
+                      head_dim, has_c2p, has_p2c) -> None:
+    """Host checks of ``deberta_attention_rel``'s tensors before anything is launched.
 
-    if batch == 0 or key_splits == 1:
+    The kernel bounds every row read by the shapes given here, so a tensor
+    that is narrower, strided differently or of another dtype than they say
+    would be read out of bounds or as garbage.
+    """
+
+    if qkv.dim() != 3:
+        raise ValueError(f"qkv must be [B, L, 3*H*d], got shape {tuple(qkv.shape)}")
+    batch, length, width = qkv.shape
+    if width != 3 * num_heads * head_dim:
+        raise ValueError(f"qkv width {width} != 3 * num_heads * head_dim = "
+                         f"{3 * num_heads * head_dim}")
+    if qkv.stride(-1) != 1 or (length > 1 and qkv.stride(1) < width) or (
+            batch > 1 and qkv.stride(0) < length * qkv.stride(1)):
+        raise ValueError(f"qkv rows must be dense in the last dimension, strides {qkv.stride()}")
+    if qkv.dtype not in SUPPORTED_DTYPES:
+        raise TypeError(f"qkv dtype {qkv.dtype} is not fp16, bf16 or fp32")
+    device = qkv.device
+    for name, table, used in (("pos_key", pos_key, has_c2p), ("pos_query", pos_query, has_p2c)):
+        if not used:
+            continue
+        if table.dtype != qkv.dtype:
+            raise TypeError(f"{name} dtype {table.dtype} does not match qkv dtype {qkv.dtype}")
+        if table.dim() != 3 or table.size(0) != num_heads or table.size(2) != head_dim:
+            raise ValueError(f"{name} must be [H={num_heads}, S, d={head_dim}], got "
+                             f"{tuple(table.shape)}")
+        if not table.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        if table.device != device:
+            raise ValueError(f"{name} is on {table.device}, qkv on {device}")
+    if has_c2p and has_p2c and pos_key.size(1) != pos_query.size(1):
+        raise ValueError("pos_key and pos_query must have the same number of active slots")
+    if delta_to_local.dtype != torch.int32 or delta_to_local.dim() != 1:
+        raise TypeError("delta_to_local must be a 1-D int32 tensor")
+    if length > 0 and delta_to_local.numel() != 2 * length - 1:
+        raise ValueError(f"delta_to_local has {delta_to_local.numel()} entries, expected "
+                         f"2L-1 = {2 * length - 1}")
+    if not delta_to_local.is_contiguous() or delta_to_local.device != device:
+        raise ValueError("delta_to_local must be contiguous and on the qkv device")
+    if attention_mask.shape != (batch, length):
+        raise ValueError(f"attention_mask shape {tuple(attention_mask.shape)} does not match "
+                         f"[{batch}, {length}]")
+    if attention_mask.element_size() != 1 or not attention_mask.is_contiguous() or (
+            attention_mask.device != device):
+        raise ValueError("attention_mask must be a contiguous bool/uint8 tensor on the qkv device")
+
+
+def _split_plan(lib, device: torch.device, dtype: torch.dtype, batch: int, heads: int,
+                length: int, head_dim: int, key_splits: int) -> tuple[int, int]:
+    """(splits, workspace bytes) for one launch; cached per device and shape.
+
+    The fp32 kernel has no split form, so fp32 never gets a workspace.
+    """
+
+    if batch == 0 or key_splits == 1 or dtype == torch.float32:
         return 1, 0
     key = (device.index, batch, heads, length, head_dim, key_splits)
     plan = _SPLIT_PLANS.get(key)

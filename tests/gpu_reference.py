@@ -1,8 +1,10 @@
 """Float64 torch statement of the fused-kernel contract, for large GPU checks.
 
-Same equation as ``oracle.attention.fused_attention`` (pinned there against the
-golden vectors), written with torch so that shapes like B=32, L=512 run on the
-GPU in float64 in well under a second.  Tests only.
+Same equation as ``oracle.attention.fused_attention``, written with torch so
+that shapes like B=32, L=512 run on the GPU in float64 in well under a second.
+``tests/test_gpu_reference_pin.py`` holds it to the golden vectors and to the
+oracle (every mode, masked rows, L=1, non-monotone tables) on the CPU.  Tests
+only.
 """
 
 from __future__ import annotations

@@ -159,52 +159,80 @@ def _encoder_inputs(batch, length, hidden, seed=19):
     return table[tokens], mask.long()
 
 
-@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
-def test_12_layer_encoder_matches_huggingface(dtype):
-    """12-layer base-shaped encoder at B=8, L=256: final hidden states vs HF.
+@pytest.fixture(scope="module")
+def base_encoder():
+    """12-layer DeBERTa-v3-base-shaped model (C3 architecture), random N(0, 0.02) init."""
 
-    The HIP encoder in ``dtype`` must stay as close to the float32 HF encoder as
-    HF's own encoder in ``dtype`` does (within 1.5x + the attention tolerance);
-    in fp32 both are held to 1e-4 on LayerNorm-scale outputs.
-    """
+    return _encoder_model(12, 768, 12, 3072)
+
+
+def _encoder_errors(base, batch, length, torch_dtype, seed=19):
+    """(hip vs HF fp32, HF-in-dtype vs HF fp32, hip vs HF-in-dtype) on valid rows."""
 
     from disentangled_flash import enable_deberta_inference
 
-    torch_dtype = DTYPES[dtype]
-    base = _encoder_model(12, 768, 12, 3072)
-    hidden, mask = _encoder_inputs(8, 256, 768)
+    hidden, mask = _encoder_inputs(batch, length, base.config.hidden_size, seed)
     hidden, mask = hidden.cuda(), mask.cuda()
     with torch.inference_mode():
         ref32 = copy.deepcopy(base).to("cuda", torch.float32).encoder
         exact = ref32(hidden.float(), mask, output_hidden_states=False).last_hidden_state
-        ref = copy.deepcopy(base).to("cuda", torch_dtype).encoder
-        same = ref(hidden.to(torch_dtype), mask, output_hidden_states=False).last_hidden_state
+        del ref32
+        if torch_dtype == torch.float32:
+            same = exact
+        else:
+            ref = copy.deepcopy(base).to("cuda", torch_dtype).encoder
+            same = ref(hidden.to(torch_dtype), mask, output_hidden_states=False).last_hidden_state
+            del ref
         fast = enable_deberta_inference(copy.deepcopy(base).to("cuda", torch_dtype),
-                                        backend="hip", sequence_lengths=[256])
+                                        backend="hip", sequence_lengths=[length])
         got = fast.encoder(hidden.to(torch_dtype), mask,
                            output_hidden_states=False).last_hidden_state
+        del fast
     valid = mask.bool()[..., None]
     err = ((got.float() - exact).abs() * valid).max().item()
     ref_err = ((same.float() - exact).abs() * valid).max().item()
     err_same = ((got.float() - same.float()).abs() * valid).max().item()
-    print(f"encoder {dtype}: hip-vs-fp32 {err:.2e}, HF-{dtype}-vs-fp32 {ref_err:.2e}, "
-          f"hip-vs-HF-{dtype} {err_same:.2e}")
+    torch.cuda.empty_cache()
+    return err, ref_err, err_same
+
+
+# Encoder tolerances.  Strict fp32 is held to the north-star limit, 1e-5 max-abs
+# on the final hidden states against Hugging Face's fp32 encoder.  In fp16/bf16
+# the HF encoder itself moves further than the attention tolerance from its
+# fp32 result over 12 layers (the reference publishes 1.56e-2 in fp16), so the
+# HIP encoder must stay as close to fp32 HF as HF's own encoder in that dtype
+# (1.5x its error plus the attention tolerance).
+ENCODER_FP32_TOL = 1e-5
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("shape", [(8, 256), (32, 512)], ids=["b8_l256", "c3_b32_l512"])
+def test_12_layer_encoder_matches_huggingface(base_encoder, dtype, shape):
+    """12-layer base-shaped encoder, final hidden states vs HF, incl. the C3 headline shape."""
+
+    torch_dtype = DTYPES[dtype]
+    batch, length = shape
+    err, ref_err, err_same = _encoder_errors(base_encoder, batch, length, torch_dtype)
+    print(f"encoder {dtype} B={batch} L={length}: hip-vs-HF-fp32 {err:.3e}, "
+          f"HF-{dtype}-vs-HF-fp32 {ref_err:.3e}, hip-vs-HF-{dtype} {err_same:.3e}")
     if torch_dtype == torch.float32:
-        assert err <= 1e-4
+        assert err <= ENCODER_FP32_TOL
     else:
         assert err <= 1.5 * ref_err + TOL[torch_dtype]
 
 
 def test_xlarge_bf16_buckets():
-    """xlarge-shaped encoder (shortened to 4 layers): hidden 1536, 24 heads, bf16, buckets."""
+    """C4: the full 24-layer xlarge-shaped encoder (hidden 1536, 24 heads, FFN 6144), bf16,
+    B=8, log-normal lengths (median 60) clipped to [16, bucket], buckets 64/128/256."""
 
     from disentangled_flash import enable_deberta_inference
 
-    base = _encoder_model(4, 1536, 24, 6144)
+    base = _encoder_model(24, 1536, 24, 6144)
     fast = enable_deberta_inference(copy.deepcopy(base).to("cuda", torch.bfloat16),
                                     backend="hip", sequence_lengths=[64, 128, 256])
     ref32 = copy.deepcopy(base).to("cuda", torch.float32).encoder
     ref16 = copy.deepcopy(base).to("cuda", torch.bfloat16).encoder
+    del base
     gen = torch.Generator().manual_seed(5)
     for bucket in (64, 128, 256):
         hidden, mask = _encoder_inputs(8, bucket, 1536, seed=bucket)
@@ -219,7 +247,7 @@ def test_xlarge_bf16_buckets():
         valid = mask.bool()[..., None]
         err = ((got.float() - exact).abs() * valid).max().item()
         ref_err = ((same.float() - exact).abs() * valid).max().item()
-        print(f"xlarge bf16 L={bucket}: hip {err:.2e}, HF bf16 {ref_err:.2e}")
+        print(f"xlarge 24-layer bf16 L={bucket}: hip {err:.3e}, HF bf16 {ref_err:.3e}")
         assert err <= 1.5 * ref_err + TOL[torch.bfloat16]
 
 
@@ -228,22 +256,34 @@ def test_optimize_deberta_on_full_model_and_compile():
 
     from disentangled_flash import compile_deberta_buckets, optimize_deberta
 
-    base = _encoder_model(2, 256, 4, 512, buckets=64).to("cuda", torch.float16)
+    base = _encoder_model(2, 256, 4, 512, buckets=64)
+    exact_model = copy.deepcopy(base).to("cuda", torch.float32)
+    base = base.to("cuda", torch.float16)
     model = optimize_deberta(copy.deepcopy(base), sequence_lengths=[64])
     ids = torch.randint(1, 1000, (4, 64), device="cuda")
     mask = (torch.arange(64, device="cuda")[None] < torch.tensor([[64], [40], [9], [1]],
                                                                  device="cuda")).long()
     with torch.inference_mode():
-        expected = base(input_ids=ids, attention_mask=mask).last_hidden_state
+        exact = exact_model(input_ids=ids, attention_mask=mask).last_hidden_state
+        same = base(input_ids=ids, attention_mask=mask).last_hidden_state
         got = model(input_ids=ids, attention_mask=mask).last_hidden_state
         hidden = model.embeddings(input_ids=ids, mask=mask)
         compiled = compile_deberta_buckets(model.encoder, [64], mode="default")
         traced = compiled[64](hidden, mask)
         eager = model.encoder(hidden, mask, output_hidden_states=False).last_hidden_state
     valid = mask.bool()[..., None]
-    assert ((got.float() - expected.float()).abs() * valid).max().item() <= 2e-2
-    # Inductor re-fuses the fp16 LayerNorm/GELU epilogues; outputs are O(1) in fp16.
-    assert (traced.float() - eager.float()).abs().max().item() <= 1e-2
+
+    def err(a, b):
+        return ((a.float() - b.float()).abs() * valid).max().item()
+
+    ref_err = err(same, exact)
+    print(f"full model fp16: hip {err(got, exact):.3e}, HF fp16 {ref_err:.3e}, compiled "
+          f"{err(traced, exact):.3e}, compiled-vs-eager {err(traced, eager):.3e}")
+    # Eager and compiled HIP paths are both held to the fp16 encoder rule against
+    # the fp32 HF model (Inductor re-fuses the torch epilogues, so the compiled
+    # bucket may round differently from the eager one, never further from fp32).
+    assert err(got, exact) <= 1.5 * ref_err + TOL[torch.float16]
+    assert err(traced, exact) <= 1.5 * ref_err + TOL[torch.float16]
 
 
 def test_hip_graph_buckets_replay_eager_results():
