@@ -33,6 +33,7 @@
 
 #include <hip/hip_runtime.h>
 #include <atomic>
+#include <mutex>
 #include <stdint.h>
 
 #include "dflash.h"
@@ -697,6 +698,17 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
 
 }  // extern "C"
 
+// ---- static scratch of the allocation-free entry point ----
+// The split-key form keeps its partial rows (fp32) in device memory between
+// the attention kernel and the merge.  dflash_attention_rel_fwd_noalloc takes
+// that memory from this file-scope array instead of from the caller, so it
+// calls no allocator.  Every GPU the library runs on holds its own copy for
+// the life of the process.  Host code never uses the array's name as an
+// address (on the host it is only a stand-in): the device address comes from
+// hipGetSymbolAddress, once per device, and is kept per device.
+constexpr size_t kScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
 
 // CU count of the current device (cached per device).
@@ -796,6 +808,28 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
   return dispatch<false>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (nullptr + error code on failure).
+int scratch_address(void** ptr) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return static_cast<int>(err);
+  if (dev < 0 || dev >= kMaxDevices) return DFLASH_ERR_SHAPE;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* addr = nullptr;
+    err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return static_cast<int>(err);
+    if (!addr) return DFLASH_ERR_NULL;
+    g_scratch_ptr[dev] = addr;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return DFLASH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -844,6 +878,43 @@ int dflash_attention_rel_fwd_split(const void* query, const void* key, const voi
                      has_c2p, has_p2c, dtype, splits, workspace, workspace_bytes, stream);
 }
 
+int dflash_attention_rel_fwd_noalloc(const void* query, const void* key, const void* value,
+                                     int64_t stride_b, int64_t stride_h, int64_t stride_l,
+                                     const void* pos_key, const void* pos_query,
+                                     const int32_t* delta_to_local,
+                                     const uint8_t* attention_mask, void* out, int B, int H,
+                                     int L, int D, int S, float score_scale_log2, int has_c2p,
+                                     int has_p2c, int dtype, int strict_fp32, int splits,
+                                     void* stream) {
+  (void)strict_fp32;
+  if (splits < 0 || splits > 8) return DFLASH_ERR_SHAPE;
+  if (B < 0 || H < 1 || L < 1) return DFLASH_ERR_SHAPE;
+  if (B == 0) return DFLASH_OK;
+  if (D != 32 && D != 64 && D != 128) return DFLASH_ERR_HEAD_DIM;
+  int count = splits;
+  if (dtype == DFLASH_DTYPE_FP32) {
+    count = 1;  // the fp32 kernel has no split form
+  } else if (count == 0) {
+    count = rel_attention_splits(B, H, L, D, current_device_cus(), nullptr);
+  } else {
+    const int tiles = (L + 63) / 64;
+    const int st = (tiles + count - 1) / count;
+    count = (tiles + st - 1) / st;
+  }
+  const size_t need = rel_attention_workspace_bytes(count, B, H, L, D);
+  if (need > kScratchBytes) return DFLASH_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (count > 1) {
+    const int rc = scratch_address(&ws);
+    if (rc != DFLASH_OK) return rc;
+  }
+  return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
+                     delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
+                     has_c2p, has_p2c, dtype, count, ws, count > 1 ? kScratchBytes : 0, stream);
+}
+
+size_t dflash_attention_rel_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
 const char* dflash_error_string(int code) {
   switch (code) {
     case DFLASH_OK:
@@ -862,6 +933,9 @@ const char* dflash_error_string(int code) {
       return "launch grid exceeds the device limit";
     case DFLASH_ERR_WORKSPACE:
       return "workspace smaller than dflash_attention_rel_split_plan reports";
+    case DFLASH_ERR_SCRATCH:
+      return "the split workspace this shape needs exceeds the library's static scratch "
+             "(dflash_attention_rel_noalloc_scratch_bytes)";
     default:
       return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }

@@ -18,7 +18,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load torch's HIP runtime first)
 
 LIBRARY_NAME = "libdflash.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_CODES = {
     torch.float16: 0,
@@ -71,6 +71,14 @@ def _bind(lib: ctypes.CDLL) -> None:
         _c_int, _c_void_p, ctypes.c_size_t,                       # splits, workspace, bytes
         _c_void_p,                                                # stream
     ]
+    lib.dflash_attention_rel_fwd_noalloc.restype = _c_int
+    lib.dflash_attention_rel_fwd_noalloc.argtypes = [
+        *lib.dflash_attention_rel_fwd.argtypes[:-1],              # as dflash_attention_rel_fwd
+        _c_int,                                                   # splits (0 = plan)
+        _c_void_p,                                                # stream
+    ]
+    lib.dflash_attention_rel_noalloc_scratch_bytes.restype = ctypes.c_size_t
+    lib.dflash_attention_rel_noalloc_scratch_bytes.argtypes = []
     lib.dflash_add_layernorm_fwd.restype = _c_int
     lib.dflash_add_layernorm_fwd.argtypes = [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, residual, gamma, beta, out

@@ -25,7 +25,7 @@ extern "C" {
 
 #define DFLASH_API __attribute__((visibility("default")))
 
-#define DFLASH_ABI_VERSION 4
+#define DFLASH_ABI_VERSION 5
 
 #define DFLASH_DTYPE_FP16 0
 #define DFLASH_DTYPE_BF16 1
@@ -39,6 +39,7 @@ extern "C" {
 #define DFLASH_ERR_ALIGN (-5)
 #define DFLASH_ERR_TOO_LARGE (-6)
 #define DFLASH_ERR_WORKSPACE (-7)
+#define DFLASH_ERR_SCRATCH (-8)
 
 /* Activation codes of the ConvLayer tail (the module's conv_act). */
 #define DFLASH_ACT_GELU 0 /* exact erf form, Hugging Face ACT2FN["gelu"] */
@@ -138,6 +139,44 @@ DFLASH_API int dflash_attention_rel_fwd_split(const void* query, const void* key
                                               int has_c2p, int has_p2c, int dtype,
                                               int strict_fp32, int splits, void* workspace,
                                               size_t workspace_bytes, void* stream);
+
+/*
+ * dflash_attention_rel_fwd_split without a caller workspace and without any
+ * allocation.
+ *
+ * No counterpart in the reference.  It is for callers that cannot allocate
+ * device memory at call time (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The partial rows of the split-key
+ * form live in a static device array of the library,
+ * dflash_attention_rel_noalloc_scratch_bytes() bytes (16 MiB) per GPU, held
+ * until the process ends; its address is looked up once per device at the
+ * first call on that device.  The function calls no hipMalloc, hipFree or
+ * allocating library routine.
+ *   splits : 0 = the count dflash_attention_rel_split_plan would choose on the
+ *            current device; 1..8 = the caller's count (as in
+ *            dflash_attention_rel_fwd_split).  fp32 never splits.
+ * Returns DFLASH_ERR_SCRATCH (nothing launched) when the split workspace of
+ * that count exceeds the scratch.  With splits = 0 on a 256-CU MI355X the
+ * plan never needs more than 8.7 MB, so only forced counts on large shapes
+ * are refused.
+ * All calls on one GPU share that GPU's scratch: calls that overlap on one
+ * GPU (on different streams, or from different host threads) race and give
+ * undefined results.  The scratch keeps the last call's contents; every call
+ * writes all the partial rows it reads, so nothing needs clearing.
+ */
+DFLASH_API int dflash_attention_rel_fwd_noalloc(const void* query, const void* key,
+                                                const void* value, int64_t stride_b,
+                                                int64_t stride_h, int64_t stride_l,
+                                                const void* pos_key, const void* pos_query,
+                                                const int32_t* delta_to_local,
+                                                const uint8_t* attention_mask, void* out, int B,
+                                                int H, int L, int D, int S,
+                                                float score_scale_log2, int has_c2p, int has_p2c,
+                                                int dtype, int strict_fp32, int splits,
+                                                void* stream);
+
+/* Size in bytes of the per-GPU static scratch of dflash_attention_rel_fwd_noalloc. */
+DFLASH_API size_t dflash_attention_rel_noalloc_scratch_bytes(void);
 
 /*
  * Fused residual add + LayerNorm of an encoder layer output.
