@@ -262,7 +262,7 @@ def bench_encoder(batch: int, length: int, steps: int, warmup: int,
             model = copy.deepcopy(base)
             enable_deberta_inference(model, backend=backend, sequence_lengths=[length])
             encoder = model.encoder
-            plans = encoder._active_plans
+            plans = encoder.active_plans
             run = lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: E731
                                                    output_hidden_states=False)
             results[f"{backend}_ms"] = time_p50(run, steps, warmup)
@@ -314,7 +314,7 @@ def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
                     lambda: base.encoder(hidden, mask, output_hidden_states=False), steps, warmup)
                 for backend, encoder in prepared.items():
                     encoder.activate_shape(length)
-                    plans = encoder._active_plans
+                    plans = encoder.active_plans
                     row[f"{backend}_ms"] = time_p50(
                         lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: B023
                                                          output_hidden_states=False),
@@ -405,7 +405,7 @@ def bench_c4(steps: int, warmup: int):
                 lambda: base.encoder(hidden, mask, output_hidden_states=False), steps, warmup)
             for backend, encoder in prepared.items():
                 encoder.activate_shape(bucket)
-                plans = encoder._active_plans
+                plans = encoder.active_plans
                 row[f"{backend}_ms"] = time_p50(
                     lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: B023
                                                      output_hidden_states=False),

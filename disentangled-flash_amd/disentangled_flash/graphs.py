@@ -31,7 +31,7 @@ class DebertaGraphBucket:
 
     def __init__(self, encoder: DebertaV2InferenceEncoder, batch: int, seq_len: int,
                  mask_dtype: torch.dtype = torch.long, warmup: int = 2) -> None:
-        if seq_len not in encoder._prepared_plans:
+        if seq_len not in encoder.prepared_lengths:
             raise ValueError(f"sequence length {seq_len} is not a prepared bucket")
         if batch < 1:
             raise ValueError("batch must be positive")
@@ -46,7 +46,7 @@ class DebertaGraphBucket:
         self.hidden_states = torch.zeros(batch, seq_len, hidden, device=weight.device,
                                          dtype=weight.dtype)
         self.attention_mask = torch.ones(batch, seq_len, device=weight.device, dtype=mask_dtype)
-        plans = encoder._prepared_plans[seq_len]
+        plans = encoder.plans_for(seq_len)
 
         def run() -> torch.Tensor:
             return encoder.forward_prepared(self.hidden_states, self.attention_mask, plans,

@@ -24,12 +24,11 @@ import ctypes
 from typing import Any, NamedTuple
 
 import torch
-from torch.nn import functional as F
 
 from . import _lib
 from ._torch import TorchInferenceDisentangledSelfAttention
 from .modeling import DebertaAttentionConfig
-from .position import SharedPositionPlanCache, canonical_device
+from .position import SharedPositionPlanCache
 
 LOG2E = 1.4426950408889634
 SUPPORTED_HEAD_DIMS = (32, 64, 128)
@@ -330,41 +329,23 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
             raise ValueError(f"relative_mode must be one of {RELATIVE_MODES}")
         self.fp32_precision = fp32_precision
         self.relative_mode = relative_mode
-        self._hip_position_projection_cache: dict[tuple[int, str], HipPreparedPositionPlan] = {}
-
-    def clear_inference_cache(self) -> None:
-        super().clear_inference_cache()
-        if hasattr(self, "_hip_position_projection_cache"):
-            self._hip_position_projection_cache.clear()
 
     @torch.no_grad()
     def prepare_shape(
         self, sequence_length: int, device: torch.device | str | None = None
     ) -> HipPreparedPositionPlan:
-        """Prepare the ``O(L)`` plan: LUT plus the active rows of the projected table."""
+        """Prepare the ``O(L)`` plan: LUT plus the active rows of the projected tables."""
 
-        if self.training:
-            raise RuntimeError("prepare_shape() requires module.eval()")
-        resolved = canonical_device(device, self._plan_device())
-        if resolved.type != "cuda":
-            raise ValueError("HIP shape plans must be prepared on a GPU device")
-        key = (sequence_length, str(resolved))
-        hit = self._hip_position_projection_cache.get(key)
-        if hit is not None:
-            return hit
-        indices = self.position_plan_cache.compact(sequence_length, resolved)
-        pos_key, pos_query = self._project_active_positions(indices.active_slots)
-        lut = indices.delta_to_local.to(dtype=torch.int32).contiguous()
-        plan = HipPreparedPositionPlan(
-            sequence_length=sequence_length,
-            active_slots=indices.active_slots,
-            delta_to_local=lut,
-            pos_key=pos_key,
-            pos_query=pos_query,
-            windowed=lut_is_window_safe(lut),
-        )
-        self._hip_position_projection_cache[key] = plan
-        return plan
+        def build(length: int, resolved: torch.device) -> HipPreparedPositionPlan:
+            if resolved.type != "cuda":
+                raise ValueError("HIP shape plans must be prepared on a GPU device")
+            indices = self.position_plan_cache.compact(length, resolved)
+            pos_key, pos_query = self._project_active_positions(indices.active_slots)
+            lut = indices.delta_to_local.to(dtype=torch.int32).contiguous()
+            return HipPreparedPositionPlan(length, indices.active_slots, lut, pos_key,
+                                           pos_query, windowed=lut_is_window_safe(lut))
+
+        return self._cached_plan(sequence_length, device, build)
 
     def _validate_hip_call(self, hidden_states: torch.Tensor) -> None:
         if hidden_states.device.type != "cuda":
@@ -399,13 +380,9 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
             raise ValueError("prepared HIP plan has no content-to-position keys")
         if has_p2c and plan.pos_query is None:
             raise ValueError("prepared HIP plan has no position-to-content queries")
-        if self._cached_qkv_weight is None:
-            raise RuntimeError(
-                "fused QKV projection is not prepared; call prepare_for_inference() first"
-            )
         scale_log2 = self.score_scale_log2()
         strict = self.fp32_precision == "strict"
-        fused = F.linear(hidden_states, self._cached_qkv_weight, self._cached_qkv_bias)
+        fused = self._fused_projection(hidden_states)
         if fused.stride(-1) != 1 or fused.stride(1) != fused.size(-1):
             fused = fused.contiguous()
         if self.relative_mode == "fused" and (plan.windowed or fused.dtype != torch.float32):
@@ -469,7 +446,7 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
             raise ValueError("the HIP path supports self-attention only")
         if relative_pos is not None:
             raise ValueError("custom relative_pos tensors are not supported by the HIP path")
-        self._lazy_prepare(rel_embeddings)
+        self._ensure_prepared(rel_embeddings)
         plan = self.prepare_shape(hidden_states.size(1), hidden_states.device)
         return self.forward_prepared(hidden_states, attention_mask, plan)
 

@@ -309,7 +309,7 @@ def test_hip_graph_buckets_replay_eager_results():
             for (batch, length), bucket in buckets.items():
                 hidden, mask = _encoder_inputs(batch, length, 768, seed=100 + replay + length)
                 hidden, mask = hidden.to("cuda", torch.float16), mask.cuda()
-                plans = encoder._prepared_plans[length]
+                plans = encoder.plans_for(length)
                 eager = encoder.forward_prepared(hidden, mask, plans,
                                                  output_hidden_states=False).last_hidden_state
                 torch.cuda.synchronize()

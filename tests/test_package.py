@@ -110,6 +110,44 @@ def test_torch_backend_matches_oracle(case):
     np.testing.assert_allclose(out.numpy(), exact, atol=1e-10)
 
 
+@pytest.mark.parametrize("case", ["v3_small", "c2p_separate_buckets16", "p2c_d128_unbucketed"])
+@pytest.mark.parametrize("rel_kind", ["standard", "shifted", "4d"])
+def test_torch_backend_custom_relative_pos_matches_original(case, rel_kind):
+    """Caller-provided relative_pos (the dynamic plan path) against the HF original module."""
+
+    from disentangled_flash._torch import TorchInferenceDisentangledSelfAttention
+    from disentangled_flash.modeling import DisentangledSelfAttention, build_relative_position
+
+    spec, params, hidden, rel, mask, _ = load_case(case)
+    config = _config(spec)
+    original = DisentangledSelfAttention(config).double().eval()
+    fast = TorchInferenceDisentangledSelfAttention(config).double().eval()
+    _load_params(original, params)
+    _load_params(fast, params)
+    h = torch.from_numpy(hidden).double()
+    length = h.size(1)
+    probe = h.view(h.size(0), 1, length, -1)
+    rpos = build_relative_position(probe, probe, spec.position_buckets,
+                                   spec.max_relative_positions)       # [1, L, L]
+    if rel_kind == "shifted":
+        rpos = (rpos + 3)[0]                                           # [L, L], off-centre
+    elif rel_kind == "4d":
+        rpos = rpos[None]                                              # [1, 1, L, L]
+    m = torch.from_numpy(mask)
+    pair = m[:, None, None, :] & m[:, None, :, None]
+    r = torch.from_numpy(rel).double()
+    with torch.inference_mode():
+        want, _ = original(h, pair, relative_pos=rpos, rel_embeddings=r)
+        got, _ = fast(h, m, relative_pos=rpos, rel_embeddings=r)
+    # The original divides by sqrt(d*f) rounded to float32 (its dtype-cast scale);
+    # the prepared path uses the exact value: ~1e-7 apart.  A wrong slot would
+    # move scores by O(0.1).
+    torch.testing.assert_close(got, want, atol=1e-6, rtol=0)
+    with pytest.raises(ValueError, match="2, 3, or 4"):
+        with torch.inference_mode():
+            fast(h, m, relative_pos=rpos.reshape(-1), rel_embeddings=r)
+
+
 def test_qkv_is_always_fused_after_prepare():
     """Reference tests/test_fused_qkv.py:7-30."""
 
@@ -123,7 +161,7 @@ def test_qkv_is_always_fused_after_prepare():
     )
     module = TorchInferenceDisentangledSelfAttention(config).eval()
     module.prepare_for_inference(torch.randn(config.position_buckets * 2, config.hidden_size))
-    assert module._cached_qkv_weight.shape == (192, 64)
+    assert module.prepared.qkv_weight.shape == (192, 64)
     with torch.inference_mode():
         q, k, v = module._project_qkv(torch.randn(2, 8, 64))
     assert q.shape == k.shape == v.shape == (2, 8, 64)
@@ -140,15 +178,15 @@ def test_inference_guards_and_cache_invalidation():
     module.eval().prepare_for_inference(torch.randn(512, 64))
     with pytest.raises(RuntimeError, match="no_grad"):
         module(torch.randn(1, 4, 64), torch.ones(1, 4))
-    assert module._cached_qkv_weight is not None
+    assert module.prepared is not None
     module.load_state_dict(module.state_dict())
-    assert module._cached_qkv_weight is None
+    assert module.prepared is None
     module.prepare_for_inference(torch.randn(512, 64))
     module.double()
-    assert module._cached_qkv_weight is None
+    assert module.prepared is None
     module.prepare_for_inference(torch.randn(512, 64, dtype=torch.float64))
     module.train()
-    assert module._cached_qkv_weight is None
+    assert module.prepared is None
 
 
 def test_hip_module_validation_errors_on_cpu():
