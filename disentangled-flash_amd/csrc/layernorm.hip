@@ -36,7 +36,7 @@ __device__ inline float wave_sum(float v) {
 }
 
 // VPL = number of 4-element chunks per lane (H <= 256 * VPL).
-template <typename T, int VPL>
+template <typename T, int VPL, bool HAS_R>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
     const T* __restrict__ x, const T* __restrict__ r, const T* __restrict__ gamma,
     const T* __restrict__ beta, T* __restrict__ y, int rows, int hidden, float eps) {
@@ -54,10 +54,13 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void add_layernorm_kernel(
     const int v = lane + 64 * k;
     if (v < nvec) {
       const V a = *reinterpret_cast<const V*>(x + base + 4 * v);
-      const V b = *reinterpret_cast<const V*>(r + base + 4 * v);
+      V b{};
+      if constexpr (HAS_R) b = *reinterpret_cast<const V*>(r + base + 4 * v);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        s[k][e] = static_cast<float>(static_cast<T>(static_cast<float>(a[e]) + static_cast<float>(b[e])));
+        s[k][e] = HAS_R ? static_cast<float>(static_cast<T>(static_cast<float>(a[e]) +
+                                                            static_cast<float>(b[e])))
+                        : static_cast<float>(a[e]);
         sum += s[k][e];
       }
     } else {
@@ -112,7 +115,7 @@ __device__ inline float group_sum(float v) {
   return v;
 }
 
-template <typename T, int LANES, int CH>
+template <typename T, int LANES, int CH, bool HAS_R>
 __global__ __launch_bounds__(256) void add_layernorm_wide_kernel(
     const T* __restrict__ x, const T* __restrict__ r, const T* __restrict__ gamma,
     const T* __restrict__ beta, T* __restrict__ y, int rows, int hidden, float eps) {
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(256) void add_layernorm_wide_kernel(
     const int v = sub + LANES * k;
     if (v < nvec) {
       a[k] = *reinterpret_cast<const V*>(x + base + N * v);
-      b[k] = *reinterpret_cast<const V*>(r + base + N * v);
+      if constexpr (HAS_R) b[k] = *reinterpret_cast<const V*>(r + base + N * v);
     }
   }
   float s[CH][N];
@@ -141,9 +144,13 @@ __global__ __launch_bounds__(256) void add_layernorm_wide_kernel(
     const bool live = sub + LANES * k < nvec;
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      s[k][e] = live ? static_cast<float>(static_cast<T>(static_cast<float>(a[k][e]) +
-                                                         static_cast<float>(b[k][e])))
-                     : 0.0f;
+      if constexpr (HAS_R) {
+        s[k][e] = live ? static_cast<float>(static_cast<T>(static_cast<float>(a[k][e]) +
+                                                           static_cast<float>(b[k][e])))
+                       : 0.0f;
+      } else {
+        s[k][e] = live ? static_cast<float>(a[k][e]) : 0.0f;
+      }
       sum += s[k][e];
     }
   }
@@ -182,10 +189,16 @@ int launch_ln_wide(const void* x, const void* r, const void* gamma, const void* 
                    int rows, int hidden, float eps, hipStream_t stream) {
   constexpr int kRows = 256 / LANES;
   const int blocks = (rows + kRows - 1) / kRows;
-  hipLaunchKernelGGL((add_layernorm_wide_kernel<T, LANES, CH>), dim3(blocks), dim3(256), 0, stream,
-                     static_cast<const T*>(x), static_cast<const T*>(r),
-                     static_cast<const T*>(gamma), static_cast<const T*>(beta),
-                     static_cast<T*>(y), rows, hidden, eps);
+  if (r != nullptr)
+    hipLaunchKernelGGL((add_layernorm_wide_kernel<T, LANES, CH, true>), dim3(blocks), dim3(256),
+                       0, stream, static_cast<const T*>(x), static_cast<const T*>(r),
+                       static_cast<const T*>(gamma), static_cast<const T*>(beta),
+                       static_cast<T*>(y), rows, hidden, eps);
+  else
+    hipLaunchKernelGGL((add_layernorm_wide_kernel<T, LANES, CH, false>), dim3(blocks), dim3(256),
+                       0, stream, static_cast<const T*>(x), static_cast<const T*>(r),
+                       static_cast<const T*>(gamma), static_cast<const T*>(beta),
+                       static_cast<T*>(y), rows, hidden, eps);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -214,10 +227,16 @@ template <typename T, int VPL>
 int launch_ln(const void* x, const void* r, const void* gamma, const void* beta, void* y,
               int rows, int hidden, float eps, hipStream_t stream) {
   const int blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL((add_layernorm_kernel<T, VPL>), dim3(blocks), dim3(64 * kRowsPerBlock), 0,
-                     stream, static_cast<const T*>(x), static_cast<const T*>(r),
-                     static_cast<const T*>(gamma), static_cast<const T*>(beta),
-                     static_cast<T*>(y), rows, hidden, eps);
+  if (r != nullptr)
+    hipLaunchKernelGGL((add_layernorm_kernel<T, VPL, true>), dim3(blocks), dim3(64 * kRowsPerBlock),
+                       0, stream, static_cast<const T*>(x), static_cast<const T*>(r),
+                       static_cast<const T*>(gamma), static_cast<const T*>(beta),
+                       static_cast<T*>(y), rows, hidden, eps);
+  else
+    hipLaunchKernelGGL((add_layernorm_kernel<T, VPL, false>), dim3(blocks),
+                       dim3(64 * kRowsPerBlock), 0, stream, static_cast<const T*>(x),
+                       static_cast<const T*>(r), static_cast<const T*>(gamma),
+                       static_cast<const T*>(beta), static_cast<T*>(y), rows, hidden, eps);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -248,7 +267,7 @@ extern "C" int dflash_add_layernorm_fwd(const void* x, const void* residual, con
                                         float eps, int dtype, void* stream) {
   if (rows < 0 || hidden < 4 || hidden % 4 != 0 || hidden > 4096) return DFLASH_ERR_SHAPE;
   if (rows == 0) return DFLASH_OK;  // nothing to do; empty tensors may carry null pointers
-  if (!x || !residual || !gamma || !beta || !out) return DFLASH_ERR_NULL;
+  if (!x || !gamma || !beta || !out) return DFLASH_ERR_NULL;  // residual NULL: LayerNorm(x)
   const int esize = dtype == DFLASH_DTYPE_FP32 ? 4 : 2;
   const uintptr_t addr_or = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
                             reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(beta) |

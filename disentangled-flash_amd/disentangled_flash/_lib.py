@@ -18,7 +18,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load torch's HIP runtime first)
 
 LIBRARY_NAME = "libdflash.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_CODES = {
     torch.float16: 0,
@@ -91,6 +91,12 @@ def _bind(lib: ctypes.CDLL) -> None:
         _c_void_p, _c_void_p, _c_void_p, _c_void_p,              # residual, bias, gamma, beta
         _c_void_p, _c_void_p,                                    # mask, out
         _c_int, _c_int, _c_int, _c_float, _c_int, _c_int,        # B, L, hidden, eps, act, dtype
+        _c_void_p,                                               # stream
+    ]
+    lib.dflash_linear_fwd.restype = _c_int
+    lib.dflash_linear_fwd.argtypes = [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, weight, bias, residual, y
+        _c_int, _c_int, _c_int, _c_int, _c_int,                  # M, N, K, epilogue, dtype
         _c_void_p,                                               # stream
     ]
     lib.dflash_error_string.restype = ctypes.c_char_p

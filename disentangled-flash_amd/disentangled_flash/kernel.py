@@ -27,6 +27,7 @@ import torch
 
 from . import _lib
 from ._torch import TorchInferenceDisentangledSelfAttention
+from .layers import GEMM_BIAS, gemm_fits, gemm_rows, linear_epilogue
 from .modeling import DebertaAttentionConfig
 from .position import SharedPositionPlanCache
 
@@ -346,6 +347,24 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
                                            pos_query, windowed=lut_is_window_safe(lut))
 
         return self._cached_plan(sequence_length, device, build)
+
+    def _fused_projection(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        """Fused QKV projection ``[B, L, 3*H*d]`` (``_torch.py:284-297``).
+
+        fp16/bf16 projections of a supported width run on the hand-written gfx950
+        GEMM (``dflash_linear_fwd``); others on ``F.linear``.
+        """
+
+        prep = self._prepared
+        if prep is None:
+            raise RuntimeError(
+                "fused QKV projection is not prepared; call prepare_for_inference() first"
+            )
+        if hidden_states.device.type == "cuda" and gemm_fits(prep.qkv_weight, prep.qkv_bias) \
+                and hidden_states.dtype == prep.qkv_weight.dtype:
+            return linear_epilogue(gemm_rows(hidden_states), prep.qkv_weight, prep.qkv_bias, None,
+                                   GEMM_BIAS)
+        return super()._fused_projection(hidden_states)
 
     def _validate_hip_call(self, hidden_states: torch.Tensor) -> None:
         if hidden_states.device.type != "cuda":

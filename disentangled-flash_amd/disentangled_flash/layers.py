@@ -58,6 +58,129 @@ def _add_layernorm_fake(x, residual, weight, bias, eps):
     return torch.empty_like(x)
 
 
+@torch.library.custom_op("disentangled_flash::layernorm", mutates_args=())
+def layernorm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float) -> torch.Tensor:
+    """``LayerNorm(x)`` over the last dimension (statistics in fp32)."""
+
+    lib = _lib.load()
+    hidden = x.shape[-1]
+    rows = x.numel() // hidden if hidden else 0
+    out = torch.empty_like(x)
+    code = lib.dflash_add_layernorm_fwd(
+        x.data_ptr(), None, weight.data_ptr(), bias.data_ptr(), out.data_ptr(), rows, hidden,
+        float(eps), _lib.DTYPE_CODES[x.dtype], _lib.current_stream_handle(x.device))
+    _lib.check(code, "dflash_add_layernorm_fwd")
+    return out
+
+
+@layernorm.register_fake
+def _layernorm_fake(x, weight, bias, eps):
+    return torch.empty_like(x)
+
+
+# dflash_linear_fwd epilogues.
+GEMM_BIAS = 0
+GEMM_BIAS_GELU = 1
+GEMM_BIAS_ADD = 2
+GEMM_DTYPES = (torch.float16, torch.bfloat16)
+
+
+@torch.library.custom_op("disentangled_flash::linear_epilogue", mutates_args=())
+def linear_epilogue(
+    x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, residual: torch.Tensor | None,
+    epilogue: int
+) -> torch.Tensor:
+    """``epilogue(x @ weight.T + bias)`` on the hand-written gfx950 GEMM.
+
+    ``x`` is ``[..., K]`` with dense rows, ``weight`` the ``[N, K]`` nn.Linear
+    weight; epilogue ``GEMM_BIAS`` (plain linear), ``GEMM_BIAS_GELU`` (exact-erf
+    GELU of the dtype-rounded linear output) or ``GEMM_BIAS_ADD`` (plus
+    ``residual`` ``[..., N]``, after rounding the linear output).
+    """
+
+    lib = _lib.load()
+    k = x.shape[-1]
+    n = weight.shape[0]
+    rows = x.numel() // k if k else 0
+    out = x.new_empty(x.shape[:-1] + (n,))
+    code = lib.dflash_linear_fwd(
+        x.data_ptr(), weight.data_ptr(), bias.data_ptr(),
+        residual.data_ptr() if residual is not None else None, out.data_ptr(), rows, n, k,
+        int(epilogue), _lib.DTYPE_CODES[x.dtype], _lib.current_stream_handle(x.device))
+    _lib.check(code, "dflash_linear_fwd")
+    return out
+
+
+@linear_epilogue.register_fake
+def _linear_epilogue_fake(x, weight, bias, residual, epilogue):
+    return x.new_empty(x.shape[:-1] + (weight.shape[0],))
+
+
+def gemm_fits(weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
+    """True if ``F.linear(x, weight, bias)`` can run on :func:`linear_epilogue`.
+
+    That is: a bias, fp16 or bf16 weight and bias on a GPU, N a multiple of 128
+    or 192 (the tile widths) and K a multiple of 32 (the k-step) - every
+    projection of DeBERTa base, large and xlarge.
+    """
+
+    if bias is None or weight.dim() != 2:
+        return False
+    n, k = weight.shape
+    if weight.dtype not in GEMM_DTYPES or bias.dtype != weight.dtype:
+        return False
+    if not weight.is_contiguous() or weight.device.type != "cuda":
+        return False
+    return (n % 128 == 0 or n % 192 == 0) and k % 32 == 0
+
+
+def linear_fits(linear: nn.Module) -> bool:
+    return isinstance(linear, nn.Linear) and gemm_fits(linear.weight, linear.bias)
+
+
+def gemm_rows(x: torch.Tensor) -> torch.Tensor:
+    """``x`` with dense rows (last dimension contiguous, rows packed)."""
+
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def fusable_intermediate(module: nn.Module) -> bool:
+    """True for a Hugging Face ``DebertaV2Intermediate`` whose activation is the erf GELU.
+
+    ``dense`` must fit :func:`gemm_fits` and ``intermediate_act_fn`` must be
+    transformers' ``GELUActivation`` (``ACT2FN["gelu"]``) computing the erf form,
+    or ``torch.nn.functional.gelu`` itself.
+    """
+
+    if not linear_fits(getattr(module, "dense", None)):
+        return False
+    act = getattr(module, "intermediate_act_fn", None)
+    if act is F.gelu:
+        return True
+    if type(act).__name__ != "GELUActivation":
+        return False
+    inner = getattr(act, "act", None)
+    return inner is F.gelu or getattr(inner, "__name__", "") == "_gelu_python"
+
+
+def intermediate_block(module: nn.Module, hidden_states: torch.Tensor) -> torch.Tensor:
+    """``module(hidden_states)`` as one GEMM with the GELU in its epilogue."""
+
+    return linear_epilogue(gemm_rows(hidden_states), module.dense.weight, module.dense.bias,
+                           None, GEMM_BIAS_GELU)
+
+
+def output_block_gemm(module: nn.Module, hidden_states: torch.Tensor,
+                      input_tensor: torch.Tensor) -> torch.Tensor:
+    """``module(hidden_states, input_tensor)``: GEMM with the residual added in its
+    epilogue, then LayerNorm over the sum (one read of it instead of two)."""
+
+    summed = linear_epilogue(gemm_rows(hidden_states), module.dense.weight, module.dense.bias,
+                             gemm_rows(input_tensor), GEMM_BIAS_ADD)
+    norm = module.LayerNorm
+    return layernorm(summed, norm.weight, norm.bias, norm.eps)
+
+
 def fusable_output_block(module: nn.Module) -> bool:
     """True for a Hugging Face ``SelfOutput``/``Output`` block the fused tail can run.
 

@@ -25,7 +25,7 @@ extern "C" {
 
 #define DFLASH_API __attribute__((visibility("default")))
 
-#define DFLASH_ABI_VERSION 5
+#define DFLASH_ABI_VERSION 6
 
 #define DFLASH_DTYPE_FP16 0
 #define DFLASH_DTYPE_BF16 1
@@ -190,6 +190,8 @@ DFLASH_API size_t dflash_attention_rel_noalloc_scratch_bytes(void);
  *   x, residual, out : [rows, hidden], dtype `dtype`, contiguous
  *   gamma, beta      : [hidden], dtype `dtype` (the LayerNorm weight and bias)
  *   out = LayerNorm(T(x + residual)) with eps, statistics in fp32.
+ *   residual may be NULL: out = LayerNorm(x) (x already holds the sum, e.g. from
+ *   dflash_linear_fwd with DFLASH_GEMM_BIAS_ADD).
  * hidden must be a multiple of 4 and at most 4096; pointers 4-element aligned.
  * rows == 0 is a no-op (pointers are not inspected).
  */
@@ -221,6 +223,36 @@ DFLASH_API int dflash_conv_layer_tail_fwd(const void* z, int z_dtype, const void
                                           const void* beta, const int64_t* mask, void* out,
                                           int B, int L, int hidden, float eps, int act, int dtype,
                                           void* stream);
+
+/* Epilogue codes of dflash_linear_fwd. */
+#define DFLASH_GEMM_BIAS 0      /* y = T(x.W^T + b) */
+#define DFLASH_GEMM_BIAS_GELU 1 /* y = T(gelu_erf(T(x.W^T + b))) */
+#define DFLASH_GEMM_BIAS_ADD 2  /* y = T(T(x.W^T + b) + residual) */
+
+/*
+ * Dense projection with a fused epilogue: y[M, N] = epilogue(x[M, K] . W[N, K]^T + bias).
+ *
+ * Replaces the nn.Linear calls of the encoder layer (F.linear = hipBLASLt in
+ * the reference's torch path) together with what follows them:
+ *   DFLASH_GEMM_BIAS      : the fused QKV projection of forward_prepared
+ *                           (/root/reference/src/disentangled_flash/_torch.py:284-297,
+ *                           weight concatenated at _torch.py:112-123)
+ *   DFLASH_GEMM_BIAS_GELU : DebertaV2Intermediate, dense then exact-erf GELU
+ *                           (/root/reference/src/disentangled_flash/_reference.py:470-471)
+ *   DFLASH_GEMM_BIAS_ADD  : dense + residual of DebertaV2SelfOutput/DebertaV2Output
+ *                           before their LayerNorm (_reference.py:108-112, 482-485)
+ * The sum is rounded to the dtype before the epilogue, as nn.Linear's output is.
+ *   x        : [M, K] row-major; weight: [N, K] row-major (the nn.Linear weight)
+ *   bias     : [N]; residual: [M, N] row-major (DFLASH_GEMM_BIAS_ADD only, else may be NULL)
+ *   y        : [M, N] row-major
+ *   dtype    : fp16 or bf16 (fp32 is not supported: DFLASH_ERR_DTYPE)
+ * N must be a multiple of 192 and K of 32 (DFLASH_ERR_SHAPE otherwise; every
+ * projection of DeBERTa base/large/xlarge qualifies); x, weight, residual, y
+ * 16-byte aligned, bias 8-byte aligned.  M == 0 is a no-op.
+ */
+DFLASH_API int dflash_linear_fwd(const void* x, const void* weight, const void* bias,
+                                 const void* residual, void* y, int M, int N, int K,
+                                 int epilogue, int dtype, void* stream);
 
 /* Text for a return code of any dflash_* entry point. */
 DFLASH_API const char* dflash_error_string(int code);
