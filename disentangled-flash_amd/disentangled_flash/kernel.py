@@ -27,6 +27,7 @@ import torch
 
 from . import _lib
 from ._torch import TorchInferenceDisentangledSelfAttention
+from . import layers
 from .layers import GEMM_BIAS, gemm_fits, gemm_rows, linear_epilogue
 from .modeling import DebertaAttentionConfig
 from .position import SharedPositionPlanCache
@@ -360,7 +361,8 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
             raise RuntimeError(
                 "fused QKV projection is not prepared; call prepare_for_inference() first"
             )
-        if hidden_states.device.type == "cuda" and gemm_fits(prep.qkv_weight, prep.qkv_bias) \
+        if layers.USE_HIP_GEMM and hidden_states.device.type == "cuda" \
+                and gemm_fits(prep.qkv_weight, prep.qkv_bias) \
                 and hidden_states.dtype == prep.qkv_weight.dtype:
             return linear_epilogue(gemm_rows(hidden_states), prep.qkv_weight, prep.qkv_bias, None,
                                    GEMM_BIAS)

@@ -78,6 +78,11 @@ def _layernorm_fake(x, weight, bias, eps):
     return torch.empty_like(x)
 
 
+# Whether the encoder runs its projections on the hand-written GEMM
+# (dflash_linear_fwd) where it fits, or on hipBLASLt through F.linear; read when
+# an encoder is prepared and on every QKV projection.  A switch for A/B timing.
+USE_HIP_GEMM = True
+
 # dflash_linear_fwd epilogues.
 GEMM_BIAS = 0
 GEMM_BIAS_GELU = 1
@@ -135,7 +140,7 @@ def gemm_fits(weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
 
 
 def linear_fits(linear: nn.Module) -> bool:
-    return isinstance(linear, nn.Linear) and gemm_fits(linear.weight, linear.bias)
+    return USE_HIP_GEMM and isinstance(linear, nn.Linear) and gemm_fits(linear.weight, linear.bias)
 
 
 def gemm_rows(x: torch.Tensor) -> torch.Tensor:
