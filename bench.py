@@ -137,13 +137,13 @@ def time_p50(fn, steps: int, warmup: int) -> float:
     return statistics.median(samples)
 
 
-def fused_call(inp, has_c2p: bool = True, has_p2c: bool = True):
+def fused_call(inp, has_c2p: bool = True, has_p2c: bool = True, key_splits: int = 0):
     from disentangled_flash.kernel import deberta_attention_rel
 
     scale_log2 = LOG2E / math.sqrt((1 + int(has_c2p) + int(has_p2c)) * inp["dim"])
     return lambda: deberta_attention_rel(inp["qkv"], inp["pos_key"], inp["pos_query"], inp["lut"],
                                          inp["mask"], inp["heads"], inp["dim"], scale_log2,
-                                         has_c2p, has_p2c, True)
+                                         has_c2p, has_p2c, True, key_splits)
 
 
 def table_call(inp):
@@ -355,6 +355,45 @@ def bench_edge(steps: int, warmup: int):
     return rows
 
 
+KERNEL_SHAPES = {
+    # name: (batch, heads, length, head_dim, boundary valid lengths?)
+    "c2": (32, 12, 512, 64, False),
+    "c5_d32": (16, 16, 384, 32, True),
+    "c5_d128": (16, 8, 512, 128, True),
+}
+BOUNDARY_LENGTHS = (1, 63, 64, 65, 127, 129, 383, 384, 511, 512)
+
+
+def kernel_inputs(shape: str, dtype):
+    batch, heads, length, dim, boundary = KERNEL_SHAPES[shape]
+    return c2_inputs(dtype, padded=False, batch=batch, heads=heads, length=length, dim=dim,
+                     valid_lengths=BOUNDARY_LENGTHS if boundary else None)
+
+
+def bench_tile_sweep(steps: int, warmup: int):
+    """Per-shape tile evidence: the fused fp16 op (c2p|p2c, no split) over batch sizes for
+    d=64 (H=12, L=512), d=32 (H=16, L=384) and d=128 (H=8, L=512).  The tile the library
+    picks can be forced per process with DFLASH_REL_QW=16 or 32 (d=32 only has both)."""
+
+    import os
+
+    rows = []
+    cases = ([(64, 12, 512, b) for b in (1, 2, 4, 8, 12, 16, 24, 32, 48)]
+             + [(32, 16, 384, b) for b in (1, 4, 8, 10, 11, 12, 13, 14, 16, 24, 32)]
+             + [(128, 8, 512, b) for b in (1, 4, 8, 16, 32)])
+    for dim, heads, length, batch in cases:
+        inp = c2_inputs(torch.float16, padded=False, batch=batch, heads=heads, length=length,
+                        dim=dim)
+        ms = time_launches(fused_call(inp, key_splits=1), steps, warmup)
+        row = {"head_dim": dim, "heads": heads, "seq_len": length, "batch": batch,
+               "qw32_workgroups": batch * heads * ((length + 127) // 128),
+               "forced_qw": os.environ.get("DFLASH_REL_QW", "table"), "us": round(ms * 1e3, 2)}
+        log(json.dumps(row))
+        rows.append(row)
+        del inp
+    return rows
+
+
 def bench_c4(steps: int, warmup: int):
     """C4: 24-layer DeBERTa-v2-xlarge-shaped encoder, bf16, B=8, one batch per bucket.
 
@@ -500,6 +539,13 @@ def main() -> int:
     parser.add_argument("--kernel-only", action="store_true",
                         help="launch only the fused C2 kernel: the clock ramp, then --steps "
                              "launches (profiling driver)")
+    parser.add_argument("--kernel-shape", choices=sorted(KERNEL_SHAPES), default="c2",
+                        help="shape of --kernel-only: c2 (B=32 L=512 H=12 d=64), c5_d32 "
+                             "(B=16 L=384 H=16 d=32), c5_d128 (B=16 L=512 H=8 d=128); the C5 "
+                             "shapes mix the boundary valid lengths")
+    parser.add_argument("--kernel-dtype", choices=sorted(DTYPES), default="fp16")
+    parser.add_argument("--tile-sweep", action="store_true",
+                        help="fused op over batch sizes for d=32/64/128 (tile-table evidence)")
     parser.add_argument("--encoder-only", action="store_true",
                         help="time only the hip 12-layer encoder (profiling driver)")
     parser.add_argument("--sweep", action="store_true",
@@ -552,15 +598,19 @@ def main() -> int:
         enc = bench_encoder(32, 512, args.encoder_steps, 3, backends=("hip",))
         log(f"encoder: {enc}")
         return 0
+    if args.tile_sweep:
+        print(json.dumps({"tile_sweep": "fused fp16 c2p|p2c, unsplit, us",
+                          "rows": bench_tile_sweep(args.steps, args.warmup)}), flush=True)
+        return 0
     if args.kernel_only:
-        inp = c2_inputs(torch.float16, padded=False)
+        inp = kernel_inputs(args.kernel_shape, DTYPES[args.kernel_dtype])
         call = fused_call(inp)
         ramp_clocks(call)
         torch.cuda.synchronize()
         for _ in range(args.steps):
             call()
         torch.cuda.synchronize()
-        log(f"launched the fused C2 kernel {args.steps} times")
+        log(f"launched the fused {args.kernel_shape} kernel {args.steps} times")
         return 0
 
     # ---- headline: fused fp16 attention, C2 without padding (every FLOP real) ----

@@ -771,6 +771,7 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
     rp.has_c2p = has_c2p;
     rp.has_p2c = has_p2c;
     rp.splits = 1;
+    rp.qw = rel_attention_qw(B, H, L, D, current_device_cus());
     if (splits > 1) {
       if (splits > 8) return DFLASH_ERR_SHAPE;
       const int tiles = (L + 63) / 64;

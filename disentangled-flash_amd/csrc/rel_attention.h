@@ -27,6 +27,9 @@ struct RelParams {
   int splits;
   int split_tiles;
   float* part;
+  // Query rows per wavefront of the unsplit form at d <= 64: 32 (default) or
+  // 16 (rel_attention_qw); d = 128 always runs 16.
+  int qw;
 };
 
 // fp16 / bf16, D in {32, 64, 128}; arguments already validated by the caller.
@@ -38,5 +41,9 @@ int launch_rel_attention_16bit(const RelParams& prm, int D, int dtype, hipStream
 // need; 1 and 0 when no split pays.
 int rel_attention_splits(int B, int H, int L, int D, int cus, int* split_tiles);
 size_t rel_attention_workspace_bytes(int splits, int B, int H, int L, int D);
+
+// Query rows per wavefront for an unsplit launch (32 or 16) on a device with
+// `cus` CUs, from the measured per-shape table in rel_attention.hip.
+int rel_attention_qw(int B, int H, int L, int D, int cus);
 
 }  // namespace dflash

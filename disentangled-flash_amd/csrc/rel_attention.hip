@@ -49,6 +49,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cstdlib>
+
 #include "device_common.h"
 #include "dflash.h"
 #include "rel_attention.h"
@@ -1004,28 +1006,26 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
 namespace {
 
-// Tile configuration per head dimension: query rows per wavefront and keys
-// per tile.  d=128 halves the query rows to stay within 256 registers at two
-// wavefronts per SIMD.
-template <int D>
-constexpr int rel_queries_per_wave() {
-  return D >= 128 ? 16 : 32;
-}
+// Tile configuration: QW query rows per wavefront (32 for d <= 64, 16 for
+// d = 128 to stay within 256 registers at two wavefronts per SIMD; 16 is also
+// built for d <= 64, for grids that leave CUs idle, see rel_attention_qw), keys
+// per tile BN, V tile buffers in LDS and workgroups per CU the registers are
+// budgeted for.
 template <int D>
 constexpr int rel_block_n() {
   return 64;
 }
-// V tile buffers in LDS and workgroups per CU the registers are budgeted for.
 // d = 128 keeps one V buffer so that two workgroups fit in the LDS of a CU
 // (65 KB each instead of 82 KB): 153 -> 117 us at B=16, L=512, H=8, fp16.
-// For d <= 64 (two workgroups either way) both placements time the same.
-template <int D>
+// For d <= 64 at QW = 32 (two workgroups either way) both placements time the
+// same; at QW = 16 one buffer lets three workgroups share a CU (48 KB each).
+template <int D, int QW>
 constexpr int rel_v_buffers() {
-  return D >= 128 ? 1 : 2;
+  return (D >= 128 || QW == 16) ? 1 : 2;
 }
-template <int D>
+template <int D, int QW>
 constexpr int rel_workgroups_per_cu() {
-  return 2;
+  return (D <= 64 && QW == 16) ? 3 : 2;
 }
 
 constexpr int kMaxKeySplits = 8;
@@ -1076,29 +1076,37 @@ __global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __res
   *reinterpret_cast<Quad<T>*>(out + row * D + d0) = q;
 }
 
-template <typename T, int D, bool C2P, bool P2C>
+template <typename T, int D, int QW, bool C2P, bool P2C>
 int launch_rel(const RelParams& base, hipStream_t stream) {
-  constexpr int QW = rel_queries_per_wave<D>();
   constexpr int BN = rel_block_n<D>();
-  constexpr int VB = rel_v_buffers<D>();
-  constexpr int WGS = rel_workgroups_per_cu<D>();
+  constexpr int VB = rel_v_buffers<D, QW>();
+  constexpr int WGS = rel_workgroups_per_cu<D, QW>();
   using LY = RelLayout<T, D, QW, BN, VB>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
+  // The split-key form exists for the default tile (QW = 32 at d <= 64, 16 at d = 128).
+  constexpr bool kSplitBuilt = (D >= 128) || QW == 32;
   constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false>;
-  constexpr auto split_kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, true>;
   if (prm.splits < 1) prm.splits = 1;
-  hipError_t err = prm.splits > 1 ? ensure_dynamic_lds<split_kernel>(static_cast<int>(LY::bytes))
-                                  : ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
-  if (err != hipSuccess) return static_cast<int>(err);
+  if (!kSplitBuilt && prm.splits > 1) return DFLASH_ERR_SHAPE;
+  hipError_t err = hipSuccess;
   const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H * prm.splits;
   if (blocks > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;
-  if (prm.splits > 1)
-    hipLaunchKernelGGL(split_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                       LY::bytes, stream, prm);
-  else
+  if constexpr (kSplitBuilt) {
+    constexpr auto split_kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, true>;
+    if (prm.splits > 1) {
+      err = ensure_dynamic_lds<split_kernel>(static_cast<int>(LY::bytes));
+      if (err != hipSuccess) return static_cast<int>(err);
+      hipLaunchKernelGGL(split_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                         LY::bytes, stream, prm);
+    }
+  }
+  if (prm.splits <= 1) {
+    err = ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
+    if (err != hipSuccess) return static_cast<int>(err);
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), LY::bytes,
                        stream, prm);
+  }
   err = hipGetLastError();
   if (err != hipSuccess || prm.splits == 1) return static_cast<int>(err);
   const int64_t rows = static_cast<int64_t>(prm.B) * prm.L * prm.H;
@@ -1109,12 +1117,28 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   return static_cast<int>(hipGetLastError());
 }
 
+template <typename T, int D, int QW>
+int rel_modes_qw(const RelParams& prm, hipStream_t stream) {
+  if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true>(prm, stream);
+  if (prm.has_c2p) return launch_rel<T, D, QW, true, false>(prm, stream);
+  if (prm.has_p2c) return launch_rel<T, D, QW, false, true>(prm, stream);
+  return launch_rel<T, D, QW, false, false>(prm, stream);
+}
+
+// d = 128 has only QW = 16; d = 32 runs QW = 16 when prm.qw asks for it (only
+// for the unsplit form: the split instances are built for QW = 32); d = 64 has
+// only QW = 32 (QW = 16 measured 1.2-2.5x slower at every batch, see
+// rel_attention_qw).
 template <typename T, int D>
 int rel_modes(const RelParams& prm, hipStream_t stream) {
-  if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, true, true>(prm, stream);
-  if (prm.has_c2p) return launch_rel<T, D, true, false>(prm, stream);
-  if (prm.has_p2c) return launch_rel<T, D, false, true>(prm, stream);
-  return launch_rel<T, D, false, false>(prm, stream);
+  if constexpr (D >= 128) {
+    return rel_modes_qw<T, D, 16>(prm, stream);
+  } else if constexpr (D == 32) {
+    if (prm.qw == 16 && prm.splits <= 1) return rel_modes_qw<T, D, 16>(prm, stream);
+    return rel_modes_qw<T, D, 32>(prm, stream);
+  } else {
+    return rel_modes_qw<T, D, 32>(prm, stream);
+  }
 }
 
 }  // namespace
@@ -1141,6 +1165,32 @@ int rel_attention_splits(int B, int H, int L, int D, int cus, int* split_tiles) 
   const int st = (tiles + splits - 1) / splits;
   if (split_tiles) *split_tiles = st;
   return (tiles + st - 1) / st;
+}
+
+int rel_attention_qw(int B, int H, int L, int D, int cus) {
+  if (D >= 128) return 16;
+  // DFLASH_REL_QW=16 or 32 forces the tile (measurement runs only).
+  static const int forced = [] {
+    const char* env = std::getenv("DFLASH_REL_QW");
+    return env ? std::atoi(env) : 0;
+  }();
+  if (forced == 16 || forced == 32) return forced;
+  // Measured table (MI355X, 256 CUs, fp16, c2p|p2c; kernel time of back-to-back
+  // launches, QW = 32 against QW = 16):
+  //   d = 64, H = 12, L = 512, B = 1..48: QW = 32 wins everywhere (QW = 16 at
+  //     three workgroups per CU is 1.2-2.5x slower: per-workgroup fixed costs
+  //     double while the MFMA work per workgroup halves).
+  //   d = 32, H = 16, L = 384: QW = 32 runs 19.0 us while its grid fits one
+  //     round of two workgroups per CU (B <= 10, 480 workgroups) and 27.0-27.6 us
+  //     at B = 11..16 (528..768); QW = 16 at three workgroups per CU runs
+  //     25.1-25.4 us at B = 11..13 (528..624 workgroups of QW = 32) and
+  //     28.7-29.2 us at B = 14..16.  So QW = 16 pays exactly when the QW = 32
+  //     grid overflows one round by at most a quarter.
+  // Grids are counted in QW = 32 workgroups (4 * 32 query rows of one (b, h)).
+  if (D != 32 || cus <= 0) return 32;
+  const int64_t wg32 = static_cast<int64_t>((L + 127) / 128) * B * H;
+  const int64_t round = 2 * static_cast<int64_t>(cus);
+  return (wg32 > round && 4 * wg32 <= 5 * round) ? 16 : 32;
 }
 
 size_t rel_attention_workspace_bytes(int splits, int B, int H, int L, int D) {

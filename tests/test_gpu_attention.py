@@ -372,3 +372,55 @@ def test_rel_kernel_random_shapes(case):
     _check(out, *args, has_c2p, has_p2c,
            f"case {case}: B={batch} H={heads} L={length} d={dim} {dtype} {pattern} "
            f"c2p={has_c2p} p2c={has_p2c} splits={splits}")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("mode", ["both", "c2p", "p2c"])
+def test_d32_tile_table_selects_qw16(dtype, mode):
+    """C5 d=32 (H=16, L=384) at B=12: the per-shape table picks the 16-row tile.
+
+    576 workgroups of the 32-row tile overflow one round of 512 slots by an
+    eighth, where the 16-row tile at three workgroups per CU was measured faster.
+    """
+
+    from disentangled_flash import _lib  # noqa: F401  (library loaded by the op)
+
+    has_c2p, has_p2c = MODES[mode]
+    args = _inputs(12, 16, 384, 32, DTYPES[dtype], "boundary", seed=12)
+    out = _run_rel(*args, has_c2p, has_p2c)
+    _check(out, *args, has_c2p, has_p2c, f"d32 B=12 qw16 {dtype} {mode}")
+
+
+QW16_SCRIPT = r"""
+import math, sys, torch
+sys.path[:0] = [{repo!r}, {pkg!r}, {tests!r}]
+import test_gpu_attention as t
+for dtype in (torch.float16, torch.bfloat16):
+    for pattern in ("right", "left", "holes", "middle", "all", "boundary"):
+        for mode, (c2p, p2c) in t.MODES.items():
+            for batch, length in ((2, 200), (3, 1), (2, 65), (1, 700)):
+                args = t._inputs(batch, 4, length, 32, dtype, pattern, seed=length + batch)
+                out = t._run_rel(*args, c2p, p2c, 1)
+                t._check(out, *args, c2p, p2c, f"qw16 {{dtype}} {{pattern}} {{mode}} B={{batch}} L={{length}}")
+print("qw16 ok", flush=True)
+"""
+
+
+def test_qw16_tile_forced_parity_subprocess():
+    """Every mode, mask pattern and length on the 16-row d=32 tile, forced by
+    DFLASH_REL_QW=16 in a child process (the tile is chosen once per process)."""
+
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    tests = Path(__file__).resolve().parent
+    repo = tests.parent
+    script = QW16_SCRIPT.format(repo=str(repo), pkg=str(repo / "disentangled-flash_amd"),
+                                tests=str(tests))
+    env = dict(os.environ, DFLASH_REL_QW="16")
+    result = subprocess.run([sys.executable, "-c", script], env=env, capture_output=True,
+                            text=True, timeout=240)
+    assert result.returncode == 0, result.stdout[-2000:] + result.stderr[-4000:]
+    assert "qw16 ok" in result.stdout
