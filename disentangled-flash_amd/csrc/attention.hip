@@ -750,63 +750,44 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
                             reinterpret_cast<uintptr_t>(pos_key) |
                             reinterpret_cast<uintptr_t>(pos_query);
   if (addr_or % 16 != 0) return DFLASH_ERR_ALIGN;
-  if (dtype != DFLASH_DTYPE_FP32) {  // fp16 / bf16: per-delta relative windows
-    RelParams rp{};
-    rp.q = query;
-    rp.k = key;
-    rp.v = value;
-    rp.sb = stride_b;
-    rp.sh = stride_h;
-    rp.sl = stride_l;
-    rp.pos_key = has_c2p ? pos_key : query;
-    rp.pos_query = has_p2c ? pos_query : key;
-    rp.lut = delta_to_local;
-    rp.mask = attention_mask;
-    rp.out = out;
-    rp.B = B;
-    rp.H = H;
-    rp.L = L;
-    rp.S = (has_c2p || has_p2c) ? S : 1;
-    rp.scale_log2 = score_scale_log2;
-    rp.has_c2p = has_c2p;
-    rp.has_p2c = has_p2c;
-    rp.splits = 1;
-    rp.qw = rel_attention_qw(B, H, L, D, current_device_cus());
-    if (splits > 1) {
-      if (splits > 8) return DFLASH_ERR_SHAPE;
-      const int tiles = (L + 63) / 64;
-      const int st = (tiles + splits - 1) / splits;
-      const int eff = (tiles + st - 1) / st;
-      if (eff > 1) {
-        if (!workspace) return DFLASH_ERR_NULL;
-        if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return DFLASH_ERR_ALIGN;
-        if (workspace_bytes < rel_attention_workspace_bytes(eff, B, H, L, D))
-          return DFLASH_ERR_WORKSPACE;
-        rp.splits = eff;
-        rp.split_tiles = st;
-        rp.part = static_cast<float*>(workspace);
-      }
+  // Every dtype runs the per-delta relative-window kernel (rel_attention.hip).
+  RelParams rp{};
+  rp.q = query;
+  rp.k = key;
+  rp.v = value;
+  rp.sb = stride_b;
+  rp.sh = stride_h;
+  rp.sl = stride_l;
+  rp.pos_key = has_c2p ? pos_key : query;
+  rp.pos_query = has_p2c ? pos_query : key;
+  rp.lut = delta_to_local;
+  rp.mask = attention_mask;
+  rp.out = out;
+  rp.B = B;
+  rp.H = H;
+  rp.L = L;
+  rp.S = (has_c2p || has_p2c) ? S : 1;
+  rp.scale_log2 = score_scale_log2;
+  rp.has_c2p = has_c2p;
+  rp.has_p2c = has_p2c;
+  rp.splits = 1;
+  rp.qw = rel_attention_qw(B, H, L, D, current_device_cus());
+  if (splits > 1 && dtype != DFLASH_DTYPE_FP32) {  // fp32 runs unsplit
+    if (splits > 8) return DFLASH_ERR_SHAPE;
+    const int tiles = (L + 63) / 64;
+    const int st = (tiles + splits - 1) / splits;
+    const int eff = (tiles + st - 1) / st;
+    if (eff > 1) {
+      if (!workspace) return DFLASH_ERR_NULL;
+      if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return DFLASH_ERR_ALIGN;
+      if (workspace_bytes < rel_attention_workspace_bytes(eff, B, H, L, D))
+        return DFLASH_ERR_WORKSPACE;
+      rp.splits = eff;
+      rp.split_tiles = st;
+      rp.part = static_cast<float*>(workspace);
     }
-    return launch_rel_attention_16bit(rp, D, dtype, static_cast<hipStream_t>(stream));
   }
-  Params prm{};
-  prm.q = query;
-  prm.k = key;
-  prm.v = value;
-  prm.sb = stride_b;
-  prm.sh = stride_h;
-  prm.sl = stride_l;
-  prm.pos_key = has_c2p ? pos_key : query;
-  prm.pos_query = has_p2c ? pos_query : key;
-  prm.lut = delta_to_local;
-  prm.mask = attention_mask;
-  prm.out = out;
-  prm.B = B;
-  prm.H = H;
-  prm.L = L;
-  prm.S = (has_c2p || has_p2c) ? S : 1;
-  prm.scale_log2 = score_scale_log2;
-  return dispatch<false>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
+  return launch_rel_attention(rp, D, dtype, static_cast<hipStream_t>(stream));
 }
 
 constexpr int kMaxDevices = 64;

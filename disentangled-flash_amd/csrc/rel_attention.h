@@ -32,9 +32,10 @@ struct RelParams {
   int qw;
 };
 
-// fp16 / bf16, D in {32, 64, 128}; arguments already validated by the caller.
-// prm.splits / split_tiles / part select the split-key form (with its merge).
-int launch_rel_attention_16bit(const RelParams& prm, int D, int dtype, hipStream_t stream);
+// fp16 / bf16 / fp32, D in {32, 64, 128}; arguments already validated by the
+// caller.  prm.splits / split_tiles / part select the split-key form (with its
+// merge; 16-bit types only).
+int launch_rel_attention(const RelParams& prm, int D, int dtype, hipStream_t stream);
 
 // Key splits for a launch of B*H query-block rows that would leave the GPU
 // underfilled (fewer workgroups than two per CU), and the workspace bytes they

@@ -84,14 +84,56 @@ __device__ inline uint8_t load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
 }
 
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
+
+// Operand traits of the kernel: one k-step is 32 deep, and a lane's operand
+// fragment holds 8 consecutive k of its row or column (k = 8g .. 8g+7 for lane
+// group g).  16-bit T: one v_mfma_f32_16x16x32_{f16,bf16}, fragment 16 bytes.
+// fp32: eight chained v_mfma_f32_16x16x4_f32, fragment 32 bytes; element e of
+// every lane's fragment feeds MFMA e, where lane (c, g) contributes k = 8g + e
+// in both operands, so the eight MFMAs sum exactly the 32 products of the step.
 template <typename T>
-__device__ inline typename Mma<T>::frag as_frag(u32x4_t v) {
-  return __builtin_bit_cast(typename Mma<T>::frag, v);
+struct RelMma {
+  using frag = typename Mma<T>::frag;
+  __device__ static f32x4_t run(frag a, frag b, f32x4_t c) { return Mma<T>::run(a, b, c); }
+};
+template <>
+struct RelMma<float> {
+  using frag = f32x8_t;
+  __device__ static f32x4_t run(frag a, frag b, f32x4_t c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], c, 0, 0, 0);
+    return c;
+  }
+};
+
+// Elements of T per 16-byte chunk.
+template <typename T>
+constexpr int kChunkElems = 16 / static_cast<int>(sizeof(T));
+
+// One lane's operand fragment from global memory (16 or 32 bytes at `off`).
+template <typename T>
+__device__ inline typename RelMma<T>::frag load_frag(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4_t lo = load16(r, off);
+    const u32x4_t hi = load16(r, off + 16);
+    return __builtin_bit_cast(f32x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  } else {
+    return __builtin_bit_cast(typename RelMma<T>::frag, load16(r, off));
+  }
+}
+
+// The elements of one 16-byte chunk.
+template <typename T>
+__device__ inline auto chunk_elems(u32x4_t v) {
+  typedef T V __attribute__((ext_vector_type(kChunkElems<T>)));
+  return __builtin_bit_cast(V, v);
 }
 
 template <typename T>
-__device__ inline typename Mma<T>::frag ones_frag() {
-  typename Mma<T>::frag f;
+__device__ inline typename RelMma<T>::frag ones_frag() {
+  typename RelMma<T>::frag f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) f[e] = static_cast<T>(1.0f);
   return f;
@@ -109,7 +151,9 @@ __device__ inline void store4(T* dst, f32x4_t acc) {
 // s + a + b with a, b in T: one dot2 against (1, 1) (exact products, fp32 sum).
 template <typename T>
 __device__ inline float add2(float s, T a, T b) {
-  if constexpr (__is_same(T, _Float16)) {
+  if constexpr (sizeof(T) == 4) {
+    return s + a + b;
+  } else if constexpr (__is_same(T, _Float16)) {
     const half2_t v = {a, b};
     const half2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
     return __builtin_amdgcn_fdot2(v, one, s, false);
@@ -176,15 +220,16 @@ struct RelLayout {
 
 template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C, bool SPLIT>
 __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
-  using M = Mma<T>;
+  using M = RelMma<T>;
   using F = typename M::frag;
+  constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
   using LY = RelLayout<T, D, QW, BN, VBUFS>;
   constexpr int BM = LY::BM;
   constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
   constexpr int KB = BN / 16;           // 16-key blocks per tile
   constexpr int DB = D / 16;            // 16-dim blocks of the output
   constexpr int KD = D / 32;            // MFMA k-steps over the head dimension
-  constexpr int CPR = D / 8;            // 16-byte chunks per K row
+  constexpr int CPR = D / E16;          // 16-byte chunks per K row
   constexpr int NKC = BN * CPR;                  // 16-byte K chunks per tile
   constexpr int NCH = (NKC + kThreads - 1) / kThreads;
   constexpr int NVB = NCH;                       // 16-byte V chunks per thread (as K)
@@ -260,13 +305,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     constexpr int RG = kThreads / CPR;  // rows summed in parallel
     const int cc = tid % CPR;
     const int rg = tid / CPR;
-    float acc[8];
+    float acc[E16];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int e = 0; e < E16; ++e) acc[e] = 0.0f;
     auto add_row = [&](u32x4_t raw) {
-      const F v = as_frag<T>(raw);
+      const auto v = chunk_elems<T>(raw);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += static_cast<float>(v[e]);
+      for (int e = 0; e < E16; ++e) acc[e] += static_cast<float>(v[e]);
     };
     // Eight rows in flight per step; rows past L read as zero and add nothing.
     for (int j = rg; j < L; j += 8 * RG) {
@@ -278,13 +323,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
     lds_barrier();  // LDS of the key loop no longer read
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vred[tid * 8 + e] = acc[e];
+    for (int e = 0; e < E16; ++e) vred[tid * E16 + e] = acc[e];
     lds_barrier();
     if (tid < D) {
-      const int col = tid >> 3;
-      const int e = tid & 7;
+      const int col = tid / E16;
+      const int e = tid % E16;
       float s = 0.0f;
-      for (int r = 0; r < RG; ++r) s += vred[(r * CPR + col) * 8 + e];
+      for (int r = 0; r < RG; ++r) s += vred[(r * CPR + col) * E16 + e];
       vmean[tid] = s / static_cast<float>(L);
     }
     lds_barrier();
@@ -302,7 +347,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     const int r = t / CPR;
     const int cc = t - r * CPR;
     koff[n] = static_cast<uint32_t>(r) * sl_bytes + cc * 16;
-    kls[n] = static_cast<uint32_t>(r * LY::KS_LD + cc * 8);
+    kls[n] = static_cast<uint32_t>(r * LY::KS_LD + cc * E16);
   }
   // V chunks: the same rows and 16-byte chunks as K.
   uint32_t vls[NVB];
@@ -311,7 +356,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     const int t = tid + n * kThreads;
     const int r = t / CPR;
     const int cc = t - r * CPR;
-    vls[n] = static_cast<uint32_t>(r * LY::VS_LD + cc * 8);
+    vls[n] = static_cast<uint32_t>(r * LY::VS_LD + cc * E16);
   }
 
   // ---- relative windows ----
@@ -347,7 +392,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   };
   const uint32_t sub = (8 * g) * ES;
   auto row_frag = [&](__amdgpu_buffer_rsrc_t r, int slot, int kd) {
-    return as_frag<T>(load16(r, static_cast<uint32_t>(slot) * (D * ES) + 32 * kd * ES + sub));
+    return load_frag<T>(r, static_cast<uint32_t>(slot) * (D * ES) + 32 * kd * ES + sub);
   };
 
   int lutc[C2P ? kSlide : 1];   // next tile's new c2p chunks
@@ -389,13 +434,14 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     for (int n = 0; n < NCH; ++n)
       if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
   };
-  // V rows are 8-byte aligned only (VS_LD = D + 4): two 8-byte stores per chunk.
+  // V rows of 16-bit T are 8-byte aligned only (VS_LD = D + 4): two 8-byte
+  // stores per chunk (half a chunk = E16 / 2 elements each).
   auto stage_v = [&](T* vs) {
 #pragma unroll
     for (int n = 0; n < NVB; ++n)
       if (NKC >= kThreads || tid < NKC) {
         *reinterpret_cast<u32x2_t*>(vs + vls[n]) = u32x2_t{pv[n][0], pv[n][1]};
-        *reinterpret_cast<u32x2_t*>(vs + vls[n] + 4) = u32x2_t{pv[n][2], pv[n][3]};
+        *reinterpret_cast<u32x2_t*>(vs + vls[n] + E16 / 2) = u32x2_t{pv[n][2], pv[n][3]};
       }
   };
 
@@ -536,7 +582,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     const int i = i0w + 16 * qb + c;
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd)
-      qf[qb][kd] = as_frag<T>(load16(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
+      qf[qb][kd] = load_frag<T>(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES);
   }
   prefetch_k(jstart);
   prefetch_v(jstart);
@@ -624,7 +670,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   f32x4_t o[DB][kQB];
   // Row sums: MFMA form (all four entries equal) or this lane's part (entry 0:
   // its keys g + 4r of every block), see kRowSumValu.
-  constexpr bool kRowSumValu = D >= 128;
+  constexpr bool kRowSumValu = D >= 128 || sizeof(T) == 4;
   f32x4_t rs[kQB];
   float row_max[kQB];
 #pragma unroll
@@ -833,18 +879,29 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     // or for d <= 64, that cost more registers than it saved (+2-5 %), and they
     // are read next to their MFMAs.
     auto vt_frag = [&](int ks, int db) {
-      // Lane c of group g supplies row 32ks + 4(c>>2) + g (+16 for the upper
-      // half), columns 16db + 4(c&3) .. +3, and receives V[rows of its
-      // k-slice][16db + c] -- keys g + 4e and 16 + g + 4e, the order of the P^T
-      // operand.  The result is moved as whole dwords: assembling the operand
-      // from its 16-bit elements was compiled into wrong code.
-      const T* p_lo = vt_cur + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
-      const T* p_hi = p_lo + 16 * LY::VS_LD;
-      const u32x2_t lo = __builtin_bit_cast(
-          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
-      const u32x2_t hi = __builtin_bit_cast(
-          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
-      return __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+      if constexpr (sizeof(T) == 4) {
+        // fp32: element e holds V[key][16db + c] for the keys of the P^T
+        // operand, 32ks + g + 4e (e < 4) and 32ks + 16 + g + 4(e - 4).
+        F a;
+        const T* col = vt_cur + 16 * db + c;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          a[e] = col[(32 * ks + (e < 4 ? 0 : 16) + g + 4 * (e & 3)) * LY::VS_LD];
+        return a;
+      } else {
+        // Lane c of group g supplies row 32ks + 4(c>>2) + g (+16 for the upper
+        // half), columns 16db + 4(c&3) .. +3, and receives V[rows of its
+        // k-slice][16db + c] -- keys g + 4e and 16 + g + 4e, the order of the P^T
+        // operand.  The result is moved as whole dwords: assembling the operand
+        // from its 16-bit elements was compiled into wrong code.
+        const T* p_lo = vt_cur + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
+        const T* p_hi = p_lo + 16 * LY::VS_LD;
+        const u32x2_t lo = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
+        const u32x2_t hi = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
+        return __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+      }
     };
     constexpr bool kVtEarly = D >= 128 && !SPLIT && C2P && P2C;
     F vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
@@ -912,7 +969,10 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           pf[qb][4 + r] = static_cast<T>(sc[2 * ks + 1][qb][r]);
         }
         // Row sums of the rounded probabilities (the values PV multiplies).
-        if constexpr (kRowSumValu) {
+        if constexpr (kRowSumValu && sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rs[qb][0] += pf[qb][e];
+        } else if constexpr (kRowSumValu) {
           const u32x4_t pp = __builtin_bit_cast(u32x4_t, pf[qb]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) rs[qb][0] = sum2<T>(rs[qb][0], pp[e]);
@@ -1019,12 +1079,15 @@ constexpr int rel_block_n() {
 // (65 KB each instead of 82 KB): 153 -> 117 us at B=16, L=512, H=8, fp16.
 // For d <= 64 at QW = 32 (two workgroups either way) both placements time the
 // same; at QW = 16 one buffer lets three workgroups share a CU (48 KB each).
-template <int D, int QW>
+// fp32 (twice the LDS per element, eight MFMAs per k-step) runs one workgroup
+// per CU with up to 512 registers per lane: two V buffers except at d = 128.
+template <typename T, int D, int QW>
 constexpr int rel_v_buffers() {
-  return (D >= 128 || QW == 16) ? 1 : 2;
+  return (D >= 128 || (QW == 16 && sizeof(T) == 2)) ? 1 : 2;
 }
-template <int D, int QW>
+template <typename T, int D, int QW>
 constexpr int rel_workgroups_per_cu() {
+  if constexpr (sizeof(T) == 4) return 1;
   return (D <= 64 && QW == 16) ? 3 : 2;
 }
 
@@ -1079,13 +1142,14 @@ __global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __res
 template <typename T, int D, int QW, bool C2P, bool P2C>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
-  constexpr int VB = rel_v_buffers<D, QW>();
-  constexpr int WGS = rel_workgroups_per_cu<D, QW>();
+  constexpr int VB = rel_v_buffers<T, D, QW>();
+  constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
   using LY = RelLayout<T, D, QW, BN, VB>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
-  // The split-key form exists for the default tile (QW = 32 at d <= 64, 16 at d = 128).
-  constexpr bool kSplitBuilt = (D >= 128) || QW == 32;
+  // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
+  // 16 at d = 128); fp32 never splits.
+  constexpr bool kSplitBuilt = sizeof(T) == 2 && ((D >= 128) || QW == 32);
   constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false>;
   if (prm.splits < 1) prm.splits = 1;
   if (!kSplitBuilt && prm.splits > 1) return DFLASH_ERR_SHAPE;
@@ -1133,7 +1197,7 @@ template <typename T, int D>
 int rel_modes(const RelParams& prm, hipStream_t stream) {
   if constexpr (D >= 128) {
     return rel_modes_qw<T, D, 16>(prm, stream);
-  } else if constexpr (D == 32) {
+  } else if constexpr (D == 32 && sizeof(T) == 2) {
     if (prm.qw == 16 && prm.splits <= 1) return rel_modes_qw<T, D, 16>(prm, stream);
     return rel_modes_qw<T, D, 32>(prm, stream);
   } else {
@@ -1198,13 +1262,15 @@ size_t rel_attention_workspace_bytes(int splits, int B, int H, int L, int D) {
   return static_cast<size_t>(splits) * B * L * H * static_cast<size_t>(D + 2) * sizeof(float);
 }
 
-int launch_rel_attention_16bit(const RelParams& prm, int D, int dtype, hipStream_t stream) {
+int launch_rel_attention(const RelParams& prm, int D, int dtype, hipStream_t stream) {
 #define DFLASH_REL_CASE(TYPE, DIM) \
   if (D == DIM) return rel_modes<TYPE, DIM>(prm, stream);
   if (dtype == DFLASH_DTYPE_FP16) {
     DFLASH_REL_CASE(_Float16, 32) DFLASH_REL_CASE(_Float16, 64) DFLASH_REL_CASE(_Float16, 128)
   } else if (dtype == DFLASH_DTYPE_BF16) {
     DFLASH_REL_CASE(__bf16, 32) DFLASH_REL_CASE(__bf16, 64) DFLASH_REL_CASE(__bf16, 128)
+  } else if (dtype == DFLASH_DTYPE_FP32) {
+    DFLASH_REL_CASE(float, 32) DFLASH_REL_CASE(float, 64) DFLASH_REL_CASE(float, 128)
   } else {
     return DFLASH_ERR_DTYPE;
   }

@@ -287,21 +287,6 @@ class HipPreparedPositionPlan(NamedTuple):
     delta_to_local: torch.Tensor
     pos_key: torch.Tensor | None
     pos_query: torch.Tensor | None
-    windowed: bool = True
-
-
-def lut_is_window_safe(delta_to_local: torch.Tensor) -> bool:
-    """True if the LUT steps by 0 or 1 per delta, the fused fp32 kernel's precondition.
-
-    Every plan built from a monotone bucket function satisfies it.  The fp16/bf16
-    kernel computes relative scores per delta and accepts any LUT; an fp32 call
-    with a plan that fails this check runs through the table path instead.
-    """
-
-    if delta_to_local.numel() < 2:
-        return True
-    step = delta_to_local.diff()
-    return bool(((step >= 0) & (step <= 1)).all())
 
 
 class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttention):
@@ -344,8 +329,7 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
             indices = self.position_plan_cache.compact(length, resolved)
             pos_key, pos_query = self._project_active_positions(indices.active_slots)
             lut = indices.delta_to_local.to(dtype=torch.int32).contiguous()
-            return HipPreparedPositionPlan(length, indices.active_slots, lut, pos_key,
-                                           pos_query, windowed=lut_is_window_safe(lut))
+            return HipPreparedPositionPlan(length, indices.active_slots, lut, pos_key, pos_query)
 
         return self._cached_plan(sequence_length, device, build)
 
@@ -406,7 +390,7 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
         fused = self._fused_projection(hidden_states)
         if fused.stride(-1) != 1 or fused.stride(1) != fused.size(-1):
             fused = fused.contiguous()
-        if self.relative_mode == "fused" and (plan.windowed or fused.dtype != torch.float32):
+        if self.relative_mode == "fused":
             placeholder = plan.delta_to_local
             output = deberta_attention_rel(
                 fused,

@@ -85,12 +85,8 @@ DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const vo
  *                       stride_h = D, stride_l = 3*H*D) - no head reshape copy.
  *   pos_key, pos_query: [H, S, D] contiguous, the plan's pos_key / pos_query
  *                       (kernel.py:461-468, 522-523)
- *   delta_to_local    : as above.  For dtype fp32 it must additionally be
- *                       non-decreasing with steps of 0 or 1 (true for every plan
- *                       built from a monotone bucket function; see
- *                       position.py:89-128): the fp32 kernel maps a tile's deltas
- *                       to a contiguous slot window.  The fp16/bf16 kernel works
- *                       per delta and accepts any table.
+ *   delta_to_local    : as above; any table (the kernel builds its relative
+ *                       windows per delta, gathering rows through the table).
  * B == 0 is a no-op that returns 0 (pointers are not inspected).
  */
 DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,
@@ -126,7 +122,8 @@ DFLASH_API int dflash_attention_rel_split_plan(int B, int H, int L, int D, int* 
  *                     partial rows (fp32) between the kernel and the merge, both
  *                     launched on `stream`.  Calls that share a workspace must not
  *                     overlap.  May be NULL when splits <= 1.
- * splits <= 1 and dtype fp32 run dflash_attention_rel_fwd unchanged.
+ * splits <= 1 and dtype fp32 (which has no split form) run dflash_attention_rel_fwd
+ * unchanged.
  * Returns DFLASH_ERR_WORKSPACE when workspace_bytes is too small.
  */
 DFLASH_API int dflash_attention_rel_fwd_split(const void* query, const void* key,

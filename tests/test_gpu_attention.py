@@ -332,9 +332,9 @@ def test_empty_batch_is_a_no_op():
                                     s, 1.0, 1, 1, 0, 1, None) == -2
 
 
-@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 def test_rel_kernel_accepts_any_lut(dtype):
-    """The 16-bit kernel works per delta: a random (non-monotone) slot table is fine."""
+    """The kernel works per delta: a random (non-monotone) slot table is fine (every dtype)."""
 
     args = list(_inputs(3, 2, 200, 64, DTYPES[dtype], "right", seed=21))
     slots = args[3].shape[1]
@@ -345,7 +345,7 @@ def test_rel_kernel_accepts_any_lut(dtype):
 
 
 @pytest.mark.parametrize("length", [2048, 4096])
-@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 def test_rel_kernel_long_sequences(length, dtype):
     """Sequences far past the bucketed range (every delta beyond +-256 shares the end slots)."""
 

@@ -45,17 +45,6 @@ def test_position_plan_matches_oracle():
         cache.compact(0, "cpu")
 
 
-def test_window_precondition_holds_for_standard_plans():
-    from disentangled_flash.kernel import lut_is_window_safe
-
-    for buckets, maximum in ((256, 512), (16, 64), (-1, 16), (8, 32)):
-        span = buckets if buckets > 0 else maximum
-        _, lut = compact_plan(600, position_buckets=buckets, max_relative_positions=maximum,
-                              position_embedding_size=span)
-        assert lut_is_window_safe(torch.from_numpy(lut))
-    assert not lut_is_window_safe(torch.tensor([0, 2, 3], dtype=torch.int32))
-
-
 def _config(case_spec, **overrides):
     from disentangled_flash.modeling import DebertaAttentionConfig
 
