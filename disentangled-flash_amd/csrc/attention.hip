@@ -14,16 +14,10 @@
 // a row max / row sum then needs 16 in-register steps and two cross-lane
 // exchanges per 64 keys.
 //
-// Relative scores come from one of two sources:
-//   * TABLE: precomputed c2p/p2c tables [B, H, L, S] in HBM (the contract of
-//     the reference op, kernel.py:137-345);
-//   * windowed (default): computed inside the tile.  The bucket function is
-//     monotone in i-j, so a tile's deltas map to a contiguous slot range
-//     [lo, hi].  Each wavefront computes its own c2p window Q_w . Kr[lo..hi]^T
-//     and the workgroup computes one shared p2c window K_tile . Qr[lo..hi]^T,
-//     both with MFMA into LDS, rounded to the input dtype exactly like the
-//     reference's separate torch.matmul (kernel.py:577,583).  No [B,H,L,S] or
-//     [B,H,L,L] tensor ever reaches HBM.
+// Relative scores come from precomputed c2p/p2c tables [B, H, L, S] in HBM:
+// this kernel serves the reference op's contract (kernel.py:137-345) and the
+// relative_mode="table" data flow.  The default path computes the relative
+// scores inside the tile instead (rel_attention.hip).
 //
 // Mask semantics follow kernel.py:250-261 (Hugging Face padded-row behaviour):
 //   kept query & kept key           -> score
@@ -43,7 +37,7 @@
 
 namespace dflash {
 
-template <typename T, int D, int BN, int QW, bool C2P, bool P2C, bool TABLE>
+template <typename T, int D, int BN, int QW, bool C2P, bool P2C>
 __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
   using M = Mma<T>;
   using F = typename M::frag;
@@ -51,7 +45,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
   constexpr int kBlockM = LY::kBlockM;
   constexpr int kQB = QW / 16;         // 16-row MFMA blocks per wavefront
   constexpr bool REL = C2P || P2C;
-  constexpr bool WINDOWED = REL && !TABLE;
   constexpr int KB = BN / 16;          // 16-key blocks per tile
   constexpr int DB = D / 16;           // 16-dim blocks of the output
   constexpr int KD = D / M::K;         // MFMA steps over the head dimension
@@ -64,8 +57,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
   T* Vt = reinterpret_cast<T*>(smem + LY::vt_off);
   float* Kbias = reinterpret_cast<float*>(smem + LY::kb_off);
   int32_t* Lw = reinterpret_cast<int32_t*>(smem + LY::lw_off);
-  T* Pw = reinterpret_cast<T*>(smem + LY::pw_off);
-  T* Cw = reinterpret_cast<T*>(smem + LY::cw_off);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -122,10 +113,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
 
   const T* posk = reinterpret_cast<const T*>(p.pos_key);
   const T* posq = reinterpret_cast<const T*>(p.pos_query);
-  const T* c2p_rows = posk + static_cast<int64_t>(bh) * L * S;  // TABLE only
-  const T* p2c_rows = posq + static_cast<int64_t>(bh) * L * S;  // TABLE only
-  const T* kr = posk + static_cast<int64_t>(h) * S * D;         // windowed only
-  const T* qr = posq + static_cast<int64_t>(h) * S * D;         // windowed only
+  const T* c2p_rows = posk + static_cast<int64_t>(bh) * L * S;  // [L, S] of this (b, h)
+  const T* p2c_rows = posq + static_cast<int64_t>(bh) * L * S;
 
   // ---- per-thread prefetch registers for the next tile ----
   // K: 16-byte row chunks.  V: 4 keys x 4 dims blocks, transposed in registers
@@ -179,67 +168,8 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
     pmask_in = jm < L;
   };
 
-  // Window products run in batches of 16-slot chunks whose row fragments are
-  // fetched from global memory (L2-resident Kr/Qr) together.
-  constexpr int NSC_C = LY::WC_MAX / 16;                       // c2p chunks per wavefront
-  constexpr int CB = (12 / KD) < 1 ? 1 : ((12 / KD) > NSC_C ? NSC_C : (12 / KD));
-  constexpr int NSC_P = LY::WP_MAX / 16;                       // p2c chunks per workgroup
-  constexpr int PU = (NSC_P + kWaves - 1) / kWaves;            // p2c chunks per wavefront
-  constexpr int PB = (6 / KD) < 1 ? 1 : ((6 / KD) > PU ? PU : (6 / KD));
-
   prefetch(0);
   for (int j0 = 0; j0 < L; j0 += BN) {
-    // Delta window of this workgroup tile and of this wavefront.
-    const int dlo = i0 - (j0 + BN - 1);
-    const int dhi = i0 + kBlockM - 1 - j0;
-    int lo_p = 0, w_p = 0, lo_c = 0, w_c = 0;
-    bool identity = false;
-    if constexpr (WINDOWED) {
-      lo_p = p.lut[clampi(dlo, -(L - 1), L - 1) + L - 1];
-      w_p = p.lut[clampi(dhi, -(L - 1), L - 1) + L - 1] - lo_p + 1;
-      const int dlo_w = clampi(i0w - (j0 + BN - 1), -(L - 1), L - 1);
-      const int dhi_w = clampi(i0w + QW - 1 - j0, -(L - 1), L - 1);
-      lo_c = p.lut[dlo_w + L - 1];
-      w_c = p.lut[dhi_w + L - 1] - lo_c + 1;
-      // Every delta of the tile has its own slot (inside the un-bucketed band,
-      // no clamping): the local slot is the window index itself.
-      identity = w_p == kBlockM + BN - 1 && dlo >= -(L - 1) && dhi <= L - 1;
-      // A plan whose lookup table is not non-decreasing with steps of 0 or 1
-      // breaks the window precondition (its output is then undefined); clamp
-      // the widths to [0, MAX] so LDS writes stay inside the buffers and the
-      // row indices below stay inside [0, S).
-      w_p = max(0, min(w_p, LY::WP_MAX));
-      w_c = max(0, min(w_c, LY::WC_MAX));
-      lo_p = max(0, min(lo_p, S - 1));
-      lo_c = max(0, min(lo_c, S - 1));
-    }
-    const int nsc_p = (w_p + 15) >> 4;
-    const int nsc_c = (w_c + 15) >> 4;
-
-    // First batch of window row fragments, issued before the barrier so their
-    // latency overlaps the LDS staging below.
-    F bq[PB][KD];
-    F bk[CB][KD];
-    if constexpr (WINDOWED && P2C) {
-#pragma unroll
-      for (int u = 0; u < PB; ++u) {
-        const int sc = wave + kWaves * u;
-        const int s = min(lo_p + 16 * sc + c, S - 1);
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd)
-          bq[u][kd] = load_slice<T>(qr + (s * D + kd * M::K), g);
-      }
-    }
-    if constexpr (WINDOWED && C2P) {
-#pragma unroll
-      for (int u = 0; u < CB; ++u) {
-        const int s = min(lo_c + 16 * u + c, S - 1);
-#pragma unroll
-        for (int kd = 0; kd < KD; ++kd)
-          bk[u][kd] = load_slice<T>(kr + (s * D + kd * M::K), g);
-      }
-    }
-
     lds_barrier();  // the previous tile is done with every LDS buffer
 
     // ---- stage the prefetched tile: K, V^T, key bias, delta -> slot window ----
@@ -272,10 +202,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
 #pragma unroll
       for (int n = 0; n < NLW; ++n) {
         const int t = tid + n * kThreads;
-        // Windowed: local slots relative to the window start, clamped into the
-        // window (only a plan breaking the step precondition needs the clamp).
-        if (t < kBlockM + BN - 1)
-          Lw[t] = WINDOWED ? max(0, min(plut[n] - lo_p, LY::WP_MAX - 1)) : plut[n];
+        if (t < kBlockM + BN - 1) Lw[t] = plut[n];
       }
     }
     lds_barrier();
@@ -300,78 +227,18 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
       }
     }
 
-    // ---- relative-score windows: transposed products, 4 packed slots per lane ----
-    if constexpr (WINDOWED) {
-      if constexpr (P2C) {
-        // Pw[jr][s - lo_p] = Qr[s] . K[j0 + jr]; chunk sc belongs to wavefront sc % 4.
-        for (int base = 0; base < PU; base += PB) {
-          if (wave + kWaves * base >= nsc_p) break;
-          if (base > 0) {
-#pragma unroll
-            for (int u = 0; u < PB; ++u) {
-              const int sc = wave + kWaves * (base + u);
-              const int s = min(lo_p + 16 * sc + c, S - 1);
-#pragma unroll
-              for (int kd = 0; kd < KD; ++kd)
-                bq[u][kd] = load_slice<T>(qr + (s * D + kd * M::K), g);
-            }
-          }
-#pragma unroll
-          for (int u = 0; u < PB; ++u) {
-            const int sc = wave + kWaves * (base + u);
-            if (sc >= nsc_p) break;
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-              f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int kd = 0; kd < KD; ++kd) acc = M::run(bq[u][kd], kfrag(kb, kd), acc);
-              store_quad<T>(Pw + (16 * kb + c) * LY::PW_LD + 16 * sc + 4 * g, acc);
-            }
-          }
-        }
-      }
-      if constexpr (C2P) {
-        // Cw[wave][q][s - lo_c] = Kr[s] . Q[i0w + q], private to the wavefront.
-        T* cwp = Cw + wave * QW * LY::CW_LD;
-        for (int base = 0; base < nsc_c; base += CB) {
-          if (base > 0) {
-#pragma unroll
-            for (int u = 0; u < CB; ++u) {
-              const int s = min(lo_c + 16 * (base + u) + c, S - 1);
-#pragma unroll
-              for (int kd = 0; kd < KD; ++kd)
-                bk[u][kd] = load_slice<T>(kr + (s * D + kd * M::K), g);
-            }
-          }
-#pragma unroll
-          for (int u = 0; u < CB; ++u) {
-            if (base + u >= nsc_c) break;
-#pragma unroll
-            for (int qb = 0; qb < kQB; ++qb) {
-              f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int kd = 0; kd < KD; ++kd) acc = M::run(bk[u][kd], qf[qb][kd], acc);
-              store_quad<T>(cwp + (16 * qb + c) * LY::CW_LD + 16 * (base + u) + 4 * g, acc);
-            }
-          }
-        }
-      }
-    }
     // Next tile's K/V/LUT/mask: issued after every load this tile consumes
     // (vector-memory counters retire in order), in flight during the softmax.
     // Unconditional (the last tile re-reads clamped rows) so that no branch
     // joins pending loads, which would force early waits on them.
     prefetch(j0 + BN);
-    if constexpr (WINDOWED) lds_barrier();
 
     // ---- relative scores, scale, key bias ----
-    // LDS addresses are a per-lane base plus compile-time offsets:
-    //   window index of (i, j): i - j - dlo = lane_base + 16*(qb - kb) - r
-    //   with lane_base = wave*QW + c - 4g + BN - 1; Pw row of key j: 16kb + 4g + r.
+    // The local slot of (i, j) sits in the LDS window of lookups at
+    //   i - j - (i0 - j0 - BN + 1) = lane_base + 16*(qb - kb) - r,
+    //   lane_base = wave*QW + c - 4g + BN - 1.
     const int lane_base = wave * QW + c - 4 * g + BN - 1;
     const int32_t* lw_lane = Lw + lane_base;
-    const T* cw_lane = Cw + (wave * QW + c) * LY::CW_LD - (lo_c - lo_p);
-    const T* pw_lane = Pw + 4 * g * LY::PW_LD;
     f32x4_t kbias[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
@@ -380,60 +247,25 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(Params p) {
 
     auto relative = [&](int qb, int kb, int r, int ls) -> float {
       float add = 0.0f;
-      if constexpr (TABLE) {
-        const int i = i0w + 16 * qb + c;
-        const int j = j0 + 16 * kb + 4 * g + r;
-        const bool ok = qin[qb] && j < L;
-        if constexpr (C2P)
-          if (ok) add += to_f<T>(c2p_rows[static_cast<int64_t>(i) * S + ls]);
-        if constexpr (P2C)
-          if (ok) add += to_f<T>(p2c_rows[static_cast<int64_t>(j) * S + ls]);
-      }
+      const int i = i0w + 16 * qb + c;
+      const int j = j0 + 16 * kb + 4 * g + r;
+      const bool ok = qin[qb] && j < L;
+      if constexpr (C2P)
+        if (ok) add += to_f<T>(c2p_rows[static_cast<int64_t>(i) * S + ls]);
+      if constexpr (P2C)
+        if (ok) add += to_f<T>(p2c_rows[static_cast<int64_t>(j) * S + ls]);
       return add;
     };
-    if constexpr (WINDOWED) {
-      if (identity) {
-        // Local slot = window index: pure immediate-offset gathers.
-        const T* cw_id = cw_lane + lane_base;
-        const T* pw_id = pw_lane + lane_base;
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb)
+    for (int qb = 0; qb < kQB; ++qb)
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int off = 16 * (qb - kb) - r;
-              const T cv = C2P ? cw_id[16 * qb * LY::CW_LD + off] : static_cast<T>(0.0f);
-              const T pv2 = P2C ? pw_id[(16 * kb + r) * LY::PW_LD + off] : static_cast<T>(0.0f);
-              const float s = add_pair<T>(sc_acc[kb][qb][r], cv, pv2);
-              sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
-            }
-      } else {
-#pragma unroll
-        for (int qb = 0; qb < kQB; ++qb)
-#pragma unroll
-          for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int ls = lw_lane[16 * (qb - kb) - r];
-              const T cv = C2P ? cw_lane[16 * qb * LY::CW_LD + ls] : static_cast<T>(0.0f);
-              const T pv2 = P2C ? pw_lane[(16 * kb + r) * LY::PW_LD + ls] : static_cast<T>(0.0f);
-              const float s = add_pair<T>(sc_acc[kb][qb][r], cv, pv2);
-              sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
-            }
-      }
-    } else {
-#pragma unroll
-      for (int qb = 0; qb < kQB; ++qb)
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float s = sc_acc[kb][qb][r];
-            if constexpr (REL) s += relative(qb, kb, r, lw_lane[16 * (qb - kb) - r]);
-            sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
-          }
-    }
+        for (int r = 0; r < 4; ++r) {
+          float s = sc_acc[kb][qb][r];
+          if constexpr (REL) s += relative(qb, kb, r, lw_lane[16 * (qb - kb) - r]);
+          sc_acc[kb][qb][r] = fmaf(s, scale, kbias[kb][r]);
+        }
 
     // ---- padded and out-of-range query rows (rare; wavefront-uniform branch) ----
 #pragma unroll
@@ -580,16 +412,15 @@ constexpr int queries_per_wave() {
   return D >= 128 ? 16 : 32;
 }
 
-template <typename T, int D, bool C2P, bool P2C, bool TABLE>
+template <typename T, int D, bool C2P, bool P2C>
 int launch(const Params& base, hipStream_t stream) {
   constexpr int BN = block_n<T, D>();
   constexpr int QW = queries_per_wave<T, D>();
   using LY = Layout<T, D, BN, QW>;
-  constexpr bool WINDOWED = (C2P || P2C) && !TABLE;
   Params prm = base;
   prm.nqb = (prm.L + LY::kBlockM - 1) / LY::kBlockM;
-  const size_t lds = LY::bytes(WINDOWED);
-  constexpr auto kernel = attention_kernel<T, D, BN, QW, C2P, P2C, TABLE>;
+  constexpr size_t lds = LY::bytes;
+  constexpr auto kernel = attention_kernel<T, D, BN, QW, C2P, P2C>;
   hipError_t err = ensure_dynamic_lds<kernel>(static_cast<int>(lds));
   if (err != hipSuccess) return static_cast<int>(err);
   const int64_t blocks = static_cast<int64_t>(prm.nqb) * prm.B * prm.H;
@@ -598,36 +429,22 @@ int launch(const Params& base, hipStream_t stream) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <typename T, int D, bool TABLE>
+template <typename T, int D>
 int dispatch_modes(const Params& prm, int has_c2p, int has_p2c, hipStream_t stream) {
-  if (has_c2p && has_p2c) return launch<T, D, true, true, TABLE>(prm, stream);
-  if (has_c2p) return launch<T, D, true, false, TABLE>(prm, stream);
-  if (has_p2c) return launch<T, D, false, true, TABLE>(prm, stream);
-  return launch<T, D, false, false, TABLE>(prm, stream);
+  if (has_c2p && has_p2c) return launch<T, D, true, true>(prm, stream);
+  if (has_c2p) return launch<T, D, true, false>(prm, stream);
+  if (has_p2c) return launch<T, D, false, true>(prm, stream);
+  return launch<T, D, false, false>(prm, stream);
 }
 
-// Table mode serves every dtype; the windowed form of this kernel serves fp32
-// only (16-bit inputs run the relative-window kernel), so only its fp32
-// instances are compiled.
-template <bool TABLE>
 int dispatch(const Params& prm, int D, int dtype, int has_c2p, int has_p2c, hipStream_t stream) {
-#define DFLASH_CASE(TYPE, DIM)                                                     \
-  if (D == DIM) return dispatch_modes<TYPE, DIM, TABLE>(prm, has_c2p, has_p2c, stream);
+#define DFLASH_CASE(TYPE, DIM) \
+  if (D == DIM) return dispatch_modes<TYPE, DIM>(prm, has_c2p, has_p2c, stream);
   switch (dtype) {
     case DFLASH_DTYPE_FP16:
-      if constexpr (TABLE) {
-        DFLASH_CASE(_Float16, 32) DFLASH_CASE(_Float16, 64) DFLASH_CASE(_Float16, 128)
-      } else {
-        return DFLASH_ERR_DTYPE;
-      }
-      break;
+      DFLASH_CASE(_Float16, 32) DFLASH_CASE(_Float16, 64) DFLASH_CASE(_Float16, 128) break;
     case DFLASH_DTYPE_BF16:
-      if constexpr (TABLE) {
-        DFLASH_CASE(__bf16, 32) DFLASH_CASE(__bf16, 64) DFLASH_CASE(__bf16, 128)
-      } else {
-        return DFLASH_ERR_DTYPE;
-      }
-      break;
+      DFLASH_CASE(__bf16, 32) DFLASH_CASE(__bf16, 64) DFLASH_CASE(__bf16, 128) break;
     case DFLASH_DTYPE_FP32:
       DFLASH_CASE(float, 32) DFLASH_CASE(float, 64) DFLASH_CASE(float, 128) break;
     default:
@@ -693,7 +510,7 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
   prm.L = L;
   prm.S = (has_c2p || has_p2c) ? S : 1;
   prm.scale_log2 = score_scale_log2;
-  return dispatch<true>(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
+  return dispatch(prm, D, dtype, has_c2p, has_p2c, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

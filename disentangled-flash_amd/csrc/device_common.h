@@ -89,37 +89,14 @@ __device__ inline float to_f(T x) {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-// s + a + b for two relative scores stored in T.  For 16-bit T the pair is
-// packed into one register and added with a single dot2 against (1, 1): the
-// products are exact and the sum is accumulated in fp32, so this equals the
-// two fp32 additions of the widened values up to fp32 rounding.
-template <typename T>
-__device__ inline float add_pair(float s, T a, T b) {
-  if constexpr (sizeof(T) == 4) {
-    return s + a + b;
-  } else if constexpr (__is_same(T, _Float16)) {
-    const half2_t v = {a, b};
-    const half2_t one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
-    return __builtin_amdgcn_fdot2(v, one, s, false);
-  } else {
-    const bf16x2_t v = {a, b};
-    const bf16x2_t one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-    return __builtin_amdgcn_fdot2_f32_bf16(v, one, s, false);
-  }
-}
-
-// 16-byte global/LDS chunk copy.
-struct alignas(16) Chunk {
-  uint32_t w[4];
-};
 
 struct Params {
   const void* q;
   const void* k;
   const void* v;
   int64_t sb, sh, sl;          // element strides of q/k/v: batch, head, position
-  const void* pos_key;         // [H, S, D] (windowed) or c2p table [B, H, L, S]
-  const void* pos_query;       // [H, S, D] (windowed) or p2c table [B, H, L, S]
+  const void* pos_key;         // c2p table [B, H, L, S]
+  const void* pos_query;       // p2c table [B, H, L, S]
   const int32_t* lut;          // delta_to_local [2L-1]
   const uint8_t* mask;         // [B, L], nonzero = kept
   void* out;                   // [B, L, H*D]
@@ -133,7 +110,6 @@ template <typename T>
 constexpr int pad_of() {
   return sizeof(T) == 2 ? 8 : 4;
 }
-constexpr int round16(int x) { return (x + 15) / 16 * 16; }
 
 template <typename T, int D, int BN, int QW>
 struct Layout {
@@ -142,30 +118,18 @@ struct Layout {
   static constexpr int kPad = pad_of<T>();
   static constexpr int KS_LD = D + kPad;                         // Ks[BN][KS_LD]
   static constexpr int VT_LD = BN + 4;                           // Vt[D][VT_LD]
-  static constexpr int WP_MAX = round16(kBlockM + BN - 1);       // p2c window
-  static constexpr int PW_LD = WP_MAX + kPad;                    // Pw[BN][PW_LD]
-  static constexpr int WC_MAX = round16(kQueriesPerWave + BN - 1);  // c2p window
-  static constexpr int CW_LD = WC_MAX + kPad;                    // Cw[w][QW][CW_LD]
   static constexpr int LW_N = kBlockM + BN;                      // lut window
 
   static constexpr size_t ks_bytes = size_t(BN) * KS_LD * sizeof(T);
   static constexpr size_t vt_bytes = size_t(D) * VT_LD * sizeof(T);
-  static constexpr size_t pw_bytes = size_t(BN) * PW_LD * sizeof(T);
-  static constexpr size_t cw_bytes = size_t(kWaves) * kQueriesPerWave * CW_LD * sizeof(T);
   static constexpr size_t lw_bytes = size_t(LW_N) * sizeof(int32_t);
   static constexpr size_t kb_bytes = size_t(BN) * sizeof(float);
 
-  // Offsets; Pw/Cw exist only for the windowed kernels.
   static constexpr size_t ks_off = 0;
   static constexpr size_t vt_off = ks_off + ks_bytes;
   static constexpr size_t kb_off = vt_off + vt_bytes;
   static constexpr size_t lw_off = kb_off + kb_bytes;
-  static constexpr size_t pw_off = lw_off + lw_bytes;
-  static constexpr size_t cw_off = pw_off + pw_bytes;
-
-  static constexpr size_t bytes(bool windowed) {
-    return windowed ? cw_off + cw_bytes : pw_off;
-  }
+  static constexpr size_t bytes = lw_off + lw_bytes;
 };
 
 // Workgroup barrier that orders LDS traffic only.  __syncthreads() also waits
@@ -195,13 +159,6 @@ template <typename T>
 using Quad = T __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-template <typename T>
-__device__ inline void store_quad(T* dst, f32x4_t acc) {
-  Quad<T> q;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) q[r] = to_t<T>(acc[r]);
-  *reinterpret_cast<Quad<T>*>(dst) = q;
-}
 
 // Host: raise a kernel's dynamic LDS limit once per device (the attribute
 // persists), instead of on every launch.
