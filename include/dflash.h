@@ -243,8 +243,8 @@ DFLASH_API int dflash_conv_layer_tail_fwd(const void* z, int z_dtype, const void
  *   bias     : [N]; residual: [M, N] row-major (DFLASH_GEMM_BIAS_ADD only, else may be NULL)
  *   y        : [M, N] row-major
  *   dtype    : fp16 or bf16 (fp32 is not supported: DFLASH_ERR_DTYPE)
- * N must be a multiple of 192 and K of 32 (DFLASH_ERR_SHAPE otherwise; every
- * projection of DeBERTa base/large/xlarge qualifies); x, weight, residual, y
+ * N must be a multiple of 128 or 192 and K of 32 (DFLASH_ERR_SHAPE otherwise;
+ * every projection of DeBERTa base/large/xlarge qualifies); x, weight, residual, y
  * 16-byte aligned, bias 8-byte aligned.  M == 0 is a no-op.
  */
 DFLASH_API int dflash_linear_fwd(const void* x, const void* weight, const void* bias,
