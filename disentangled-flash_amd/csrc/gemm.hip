@@ -14,21 +14,21 @@
 //                  of DebertaV2SelfOutput / DebertaV2Output before LayerNorm,
 //                  _reference.py:108-112, 482-485)
 //
-// Tiling.  A workgroup of 4 wavefronts computes a 256 x 192 tile of Y; each
-// wavefront a 128 x 96 sub-tile (8 x 6 blocks of 16 x 16, 192 fp32
-// accumulators per lane).  K is walked in steps of 32 through a 5-stage LDS
-// ring (28 KB per stage).  Global -> LDS copies use global_load_lds_dwordx4:
-// no registers, no VALU; each instruction of a wavefront writes 1 KB of LDS in
-// lane order, so the LDS layout is chosen by which global chunk each lane
-// fetches.  Rows of the K-step are 64 bytes; two rows form a 128-byte line,
-// and the eight 16-byte chunks of a line are XOR-swizzled with the line index,
-// which makes the MFMA fragment reads (ds_read_b128, 16 rows x one k-slice per
-// 16 lanes) bank-conflict free.
+// Tiling.  A workgroup of WAVES_M x WAVES_N wavefronts computes a 256 x BN
+// tile of Y (GemmConfig below: 256 x 192 with 4 or 8 wavefronts, 256 x 128
+// with 4 wavefronts at two workgroups per CU).  K is walked in steps of 32
+// through a ring of LDS stages.  Global -> LDS copies use
+// global_load_lds_dwordx4: no registers, no VALU; each instruction of a
+// wavefront writes 1 KB of LDS in lane order, so the LDS layout is chosen by
+// which global chunk each lane fetches.  Rows of the K-step are 64 bytes; two
+// rows form a 128-byte line, and the eight 16-byte chunks of a line are
+// XOR-swizzled with the line index, which makes the MFMA fragment reads
+// (ds_read_b128, 16 rows x one k-slice per 16 lanes) bank-conflict free.
 //
 // MFMA v_mfma_f32_16x16x32_{f16,bf16} with the weight as the A operand and the
 // activation as B, so the accumulator of lane (c, g) holds Y[m0 + c][n0 + 4g ..
-// n0 + 4g + 3]: four consecutive outputs of one row, stored as one 8-byte
-// write.
+// n0 + 4g + 3]: four consecutive outputs of one row.  The epilogue stages the
+// tile through LDS and writes it in coalesced 16-byte chunks.
 //
 // Launch order: workgroup p runs on XCD p % 8.  Each XCD takes a contiguous
 // range of row blocks and walks its column blocks fastest, so the tiles of
