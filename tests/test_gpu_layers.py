@@ -56,6 +56,23 @@ def test_add_layernorm_matches_float64(dtype, rows, hidden):
     assert (out.double() - torch_out.double()).abs().max().item() <= 2 * bound.max().item()
 
 
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("rows,hidden", [(1, 768), (4096, 768), (65, 1536), (2, 36), (9, 260)])
+def test_layernorm_without_residual_matches_float64(dtype, rows, hidden):
+    """The NULL-residual form (the attention-output block after the GEMM's add)."""
+
+    from disentangled_flash.layers import layernorm
+
+    x, _, w, b = _case(rows, hidden, DTYPES[dtype], rows * 11 + hidden)
+    eps = 1e-7
+    out = layernorm(x, w, b, eps)
+    torch.cuda.synchronize()
+    ref = F.layer_norm(x.double(), (hidden,), w.double(), b.double(), eps)
+    rel, abs_tol = TOLS[x.dtype]
+    err = (out.double() - ref).abs()
+    assert bool((err <= rel * ref.abs() + abs_tol).all()), f"max err {err.max().item():.3e}"
+
+
 def test_add_layernorm_zero_rows_and_errors():
     from disentangled_flash import _lib
     from disentangled_flash.layers import add_layernorm

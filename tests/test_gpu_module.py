@@ -221,6 +221,20 @@ def test_12_layer_encoder_matches_huggingface(base_encoder, dtype, shape):
         assert err <= 1.5 * ref_err + TOL[torch_dtype]
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_encoder_with_library_projections(base_encoder, dtype, monkeypatch):
+    """The A/B switch: projections on hipBLASLt (F.linear), tails on the fused add + LayerNorm."""
+
+    from disentangled_flash import layers
+
+    monkeypatch.setattr(layers, "USE_HIP_GEMM", False)
+    torch_dtype = DTYPES[dtype]
+    err, ref_err, err_same = _encoder_errors(base_encoder, 8, 256, torch_dtype)
+    print(f"encoder (F.linear projections) {dtype}: hip-vs-HF-fp32 {err:.3e}, "
+          f"HF-{dtype}-vs-HF-fp32 {ref_err:.3e}")
+    assert err <= 1.5 * ref_err + TOL[torch_dtype]
+
+
 def test_xlarge_bf16_buckets():
     """C4: the full 24-layer xlarge-shaped encoder (hidden 1536, 24 heads, FFN 6144), bf16,
     B=8, log-normal lengths (median 60) clipped to [16, bucket], buckets 64/128/256."""
