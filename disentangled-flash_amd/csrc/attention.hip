@@ -487,7 +487,9 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
                          const uint8_t* attention_mask, void* out, int B, int H, int L, int D,
                          int S, float score_scale_log2, int has_c2p, int has_p2c, int dtype,
                          int strict_fp32, void* stream) {
-  (void)strict_fp32;  // fp32 always runs IEEE fp32 MFMA on gfx950
+  // The table contract runs IEEE fp32 MFMA for either precision; the fast
+  // fp32 form (bf16x3) is built for the in-kernel-relative entry points.
+  (void)strict_fp32;
   int rc = check_common(query, key, value, delta_to_local, attention_mask, out, B, H, L, D, S,
                         has_c2p, has_p2c, dtype);
   if (rc == kEmptyBatch) return DFLASH_OK;
@@ -550,7 +552,8 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
                 int64_t stride_h, int64_t stride_l, const void* pos_key, const void* pos_query,
                 const int32_t* delta_to_local, const uint8_t* attention_mask, void* out, int B,
                 int H, int L, int D, int S, float score_scale_log2, int has_c2p, int has_p2c,
-                int dtype, int splits, void* workspace, size_t workspace_bytes, void* stream) {
+                int dtype, int strict_fp32, int splits, void* workspace, size_t workspace_bytes,
+                void* stream) {
   int rc = check_common(query, key, value, delta_to_local, attention_mask, out, B, H, L, D, S,
                         has_c2p, has_p2c, dtype);
   if (rc == kEmptyBatch) return DFLASH_OK;
@@ -589,6 +592,7 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
   rp.has_p2c = has_p2c;
   rp.splits = 1;
   rp.qw = rel_attention_qw(B, H, L, D, current_device_cus());
+  rp.fast = dtype == DFLASH_DTYPE_FP32 && !strict_fp32;
   if (splits > 1 && dtype != DFLASH_DTYPE_FP32) {  // fp32 runs unsplit
     if (splits > 8) return DFLASH_ERR_SHAPE;
     const int tiles = (L + 63) / 64;
@@ -640,10 +644,9 @@ int dflash_attention_rel_fwd(const void* query, const void* key, const void* val
                              void* out, int B, int H, int L, int D, int S,
                              float score_scale_log2, int has_c2p, int has_p2c, int dtype,
                              int strict_fp32, void* stream) {
-  (void)strict_fp32;
   return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
                      delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
-                     has_c2p, has_p2c, dtype, 1, nullptr, 0, stream);
+                     has_c2p, has_p2c, dtype, strict_fp32, 1, nullptr, 0, stream);
 }
 
 int dflash_attention_rel_split_plan(int B, int H, int L, int D, int* splits,
@@ -671,10 +674,9 @@ int dflash_attention_rel_fwd_split(const void* query, const void* key, const voi
                                    int L, int D, int S, float score_scale_log2, int has_c2p,
                                    int has_p2c, int dtype, int strict_fp32, int splits,
                                    void* workspace, size_t workspace_bytes, void* stream) {
-  (void)strict_fp32;
   return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
                      delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
-                     has_c2p, has_p2c, dtype, splits, workspace, workspace_bytes, stream);
+                     has_c2p, has_p2c, dtype, strict_fp32, splits, workspace, workspace_bytes, stream);
 }
 
 int dflash_attention_rel_fwd_noalloc(const void* query, const void* key, const void* value,
@@ -685,7 +687,6 @@ int dflash_attention_rel_fwd_noalloc(const void* query, const void* key, const v
                                      int L, int D, int S, float score_scale_log2, int has_c2p,
                                      int has_p2c, int dtype, int strict_fp32, int splits,
                                      void* stream) {
-  (void)strict_fp32;
   if (splits < 0 || splits > 8) return DFLASH_ERR_SHAPE;
   if (B < 0 || H < 1 || L < 1) return DFLASH_ERR_SHAPE;
   if (B == 0) return DFLASH_OK;
@@ -709,7 +710,8 @@ int dflash_attention_rel_fwd_noalloc(const void* query, const void* key, const v
   }
   return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
                      delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
-                     has_c2p, has_p2c, dtype, count, ws, count > 1 ? kScratchBytes : 0, stream);
+                     has_c2p, has_p2c, dtype, strict_fp32, count, ws, count > 1 ? kScratchBytes : 0,
+                     stream);
 }
 
 size_t dflash_attention_rel_noalloc_scratch_bytes(void) { return kScratchBytes; }

@@ -30,6 +30,9 @@ struct RelParams {
   // Query rows per wavefront of the unsplit form at d <= 64: 32 (default) or
   // 16 (rel_attention_qw); d = 128 always runs 16.
   int qw;
+  // fp32 only: 1 = products on the bf16 matrix unit in three parts
+  // (fp32_precision="fast"), 0 = IEEE fp32 MFMA.
+  int fast;
 };
 
 // fp16 / bf16 / fp32, D in {32, 64, 128}; arguments already validated by the

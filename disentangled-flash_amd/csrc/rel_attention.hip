@@ -49,6 +49,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include <cstdlib>
 
 #include "device_common.h"
@@ -105,6 +107,42 @@ struct RelMma<float> {
 #pragma unroll
     for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], c, 0, 0, 0);
     return c;
+  }
+};
+
+// fp32 operands on the bf16 matrix unit (fp32_precision="fast"): each value is
+// split into x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), and the
+// product a.b is a_hi.b_hi + a_hi.b_lo + a_lo.b_hi (three
+// v_mfma_f32_16x16x32_bf16; the dropped a_lo.b_lo and the rounding of lo leave a
+// relative error of about 2^-16 per product, against 2^-11 for TF32, the
+// reference's fast mode).  The fragments are the fp32 ones (k = 8g + e in both
+// operands), which is the 16-bit instruction's k layout.
+struct RelMmaFast {
+  using frag = f32x8_t;
+  struct split_frag {
+    bf16x8_t hi, lo;
+  };
+  __device__ static split_frag split(const f32x8_t& x) {
+    split_frag s;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const __bf16 h = static_cast<__bf16>(x[e]);
+      s.hi[e] = h;
+      s.lo[e] = static_cast<__bf16>(x[e] - static_cast<float>(h));
+    }
+    return s;
+  }
+  __device__ static const split_frag& as_split(const split_frag& x) { return x; }
+  __device__ static split_frag as_split(const f32x8_t& x) { return split(x); }
+  // Operands may be fp32 fragments (split here) or fragments split once where
+  // they are produced (the ones used by several products).
+  template <typename A, typename B>
+  __device__ static f32x4_t run(const A& a, const B& b, f32x4_t c) {
+    const split_frag sa = as_split(a);
+    const split_frag sb = as_split(b);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.lo, sb.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.hi, sb.lo, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.hi, sb.hi, c, 0, 0, 0);
   }
 };
 
@@ -218,10 +256,21 @@ struct RelLayout {
 
 }  // namespace
 
-template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C, bool SPLIT>
+template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C, bool SPLIT,
+          bool FAST = false>
 __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
-  using M = RelMma<T>;
+  static_assert(!FAST || sizeof(T) == 4, "the bf16x3 form is for fp32 data");
+  using M = std::conditional_t<FAST, RelMmaFast, RelMma<T>>;
   using F = typename M::frag;
+  // Fragments that feed several products: split once in the fast fp32 form.
+  using QF = std::conditional_t<FAST, typename RelMmaFast::split_frag, F>;
+  auto to_q = [](const F& x) -> QF {
+    if constexpr (FAST) {
+      return RelMmaFast::split(x);
+    } else {
+      return x;
+    }
+  };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
   using LY = RelLayout<T, D, QW, BN, VBUFS>;
   constexpr int BM = LY::BM;
@@ -283,7 +332,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // ---- queries: fragments stay in registers (B operand of K.Q^T and Kr.Q^T) ----
   // They are loaded in the prologue, after the lookups and rows that the first
   // products wait for (loads return in issue order).
-  F qf[kQB][KD];
+  QF qf[kQB][KD];
   bool qkept[kQB];
 
   // ---- padding extent (wavefront-uniform; every wavefront derives the same values) ----
@@ -582,7 +631,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     const int i = i0w + 16 * qb + c;
 #pragma unroll
     for (int kd = 0; kd < KD; ++kd)
-      qf[qb][kd] = load_frag<T>(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES);
+      qf[qb][kd] = to_q(load_frag<T>(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
   }
   prefetch_k(jstart);
   prefetch_v(jstart);
@@ -719,9 +768,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         kfa[0][kd] = *reinterpret_cast<const F*>(Ks + key_of(c) * LY::KS_LD + 32 * kd + 8 * g);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        F kf[KD];
+        QF kf[KD];
 #pragma unroll
-        for (int kd = 0; kd < KD; ++kd) kf[kd] = kfa[kb & 1][kd];
+        for (int kd = 0; kd < KD; ++kd) kf[kd] = to_q(kfa[kb & 1][kd]);
         if (kb + 1 < KB) {
 #pragma unroll
           for (int kd = 0; kd < KD; ++kd)
@@ -759,10 +808,10 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     } else {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        F kf[KD];
+        QF kf[KD];
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd)
-          kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+          kf[kd] = to_q(*reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g));
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
           f32x4_t acc{0.f, 0.f, 0.f, 0.f};
@@ -980,6 +1029,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           rs[qb] = M::run(ones, pf[qb], rs[qb]);
         }
       }
+      QF pq[kQB];
+#pragma unroll
+      for (int qb = 0; qb < kQB; ++qb) pq[qb] = to_q(pf[qb]);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         F a;
@@ -988,8 +1040,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         } else {
           a = vt_frag(ks, db);
         }
+        const QF aq = to_q(a);
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
+        for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(aq, pq[qb], o[db][qb]);
       }
     }
 
@@ -1139,7 +1192,7 @@ __global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __res
   *reinterpret_cast<Quad<T>*>(out + row * D + d0) = q;
 }
 
-template <typename T, int D, int QW, bool C2P, bool P2C>
+template <typename T, int D, int QW, bool C2P, bool P2C, bool FAST = false>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
   constexpr int VB = rel_v_buffers<T, D, QW>();
@@ -1150,7 +1203,7 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
   // 16 at d = 128); fp32 never splits.
   constexpr bool kSplitBuilt = sizeof(T) == 2 && ((D >= 128) || QW == 32);
-  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false>;
+  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false, FAST>;
   if (prm.splits < 1) prm.splits = 1;
   if (!kSplitBuilt && prm.splits > 1) return DFLASH_ERR_SHAPE;
   hipError_t err = hipSuccess;
@@ -1181,12 +1234,15 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <typename T, int D, int QW>
+template <typename T, int D, int QW, bool FAST = false>
 int rel_modes_qw(const RelParams& prm, hipStream_t stream) {
-  if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true>(prm, stream);
-  if (prm.has_c2p) return launch_rel<T, D, QW, true, false>(prm, stream);
-  if (prm.has_p2c) return launch_rel<T, D, QW, false, true>(prm, stream);
-  return launch_rel<T, D, QW, false, false>(prm, stream);
+  if constexpr (sizeof(T) == 4 && !FAST) {
+    if (prm.fast) return rel_modes_qw<T, D, QW, true>(prm, stream);
+  }
+  if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true, FAST>(prm, stream);
+  if (prm.has_c2p) return launch_rel<T, D, QW, true, false, FAST>(prm, stream);
+  if (prm.has_p2c) return launch_rel<T, D, QW, false, true, FAST>(prm, stream);
+  return launch_rel<T, D, QW, false, false, FAST>(prm, stream);
 }
 
 // d = 128 has only QW = 16; d = 32 runs QW = 16 when prm.qw asks for it (only

@@ -59,8 +59,9 @@ extern "C" {
  *   attention_mask    : uint8 [B, L], nonzero = kept token (the reference's bool mask)
  *   out               : [B, L, H*D], dtype `dtype`
  *   score_scale_log2  : log2(e) / sqrt(D * (1 + has_c2p + has_p2c))  (kernel.py:587-588)
- *   strict_fp32       : accepted for signature parity; gfx950 has no TF32 MFMA,
- *                       so fp32 always runs IEEE fp32 MFMA.
+ *   strict_fp32       : accepted for signature parity; this table-reading
+ *                       entry point runs IEEE fp32 MFMA for either value (the
+ *                       fast fp32 form is built for dflash_attention_rel_fwd).
  * B == 0 is a no-op that returns 0 (pointers are not inspected), like the
  * reference's launch over an empty grid.
  */
@@ -87,6 +88,13 @@ DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const vo
  *                       (kernel.py:461-468, 522-523)
  *   delta_to_local    : as above; any table (the kernel builds its relative
  *                       windows per delta, gathering rows through the table).
+ *   strict_fp32       : fp32 only.  1 = IEEE fp32 MFMA (v_mfma_f32_16x16x4_f32),
+ *                       the reference's strict mode (input_precision="ieee",
+ *                       kernel.py:216).  0 = the reference's fast mode, which is
+ *                       TF32 there (kernel.py:222); gfx950 has no TF32 matrix
+ *                       path, so each fp32 operand is split into bf16 hi + lo
+ *                       and the product runs as three bf16 MFMAs (relative error
+ *                       about 2^-16 per product, below TF32's 2^-11).
  * B == 0 is a no-op that returns 0 (pointers are not inspected).
  */
 DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,

@@ -43,7 +43,7 @@ def _init(module, seed):
                 param.zero_()
 
 
-def _hip_from_hf(hf_module, cfg, dtype, mode="fused"):
+def _hip_from_hf(hf_module, cfg, dtype, mode="fused", fp32_precision="strict"):
     from disentangled_flash.kernel import HipInferenceDisentangledSelfAttention
     from disentangled_flash.modeling import DebertaAttentionConfig
 
@@ -54,7 +54,8 @@ def _hip_from_hf(hf_module, cfg, dtype, mode="fused"):
         pos_att_type=tuple(cfg.pos_att_type), share_att_key=cfg.share_att_key,
         hidden_dropout_prob=0.0, attention_probs_dropout_prob=0.0,
     )
-    module = HipInferenceDisentangledSelfAttention(config, relative_mode=mode)
+    module = HipInferenceDisentangledSelfAttention(config, relative_mode=mode,
+                                                   fp32_precision=fp32_precision)
     module.load_state_dict(hf_module.state_dict(), strict=True)
     return module.to("cuda", dtype).eval()
 
@@ -103,6 +104,26 @@ def test_c1_layer_matches_huggingface(dtype, mode):
     print(f"C1 {dtype} {mode}: vs HF same dtype {err:.2e}, vs fp64 {err64:.2e} (HF {ref_err:.2e})")
     assert err <= TOL[torch_dtype]
     assert err64 <= TOL[torch_dtype]
+
+
+# fp32_precision="fast" (bf16x3 products in the fused kernel; see
+# test_gpu_attention.TOL_FAST_FP32): module and encoder bounds.
+TOL_FAST_FP32 = 1e-4
+
+
+def test_c1_layer_fast_fp32():
+    """C1 in fp32 with fp32_precision="fast", against HF in float64."""
+
+    hf_module, cfg = _hf_attention(768, 12, 64, ("c2p", "p2c"))
+    _init(hf_module, 17)
+    gen = torch.Generator().manual_seed(18)
+    lengths = torch.randint(64, 129, (2,), generator=gen)
+    states, rel, mask = _inputs(2, 128, 768, lengths, 19, 256)
+    hip = _hip_from_hf(hf_module, cfg, torch.float32, "fused", fp32_precision="fast")
+    got, _, exact = _run_pair(hf_module, hip, states, rel, mask, torch.float32)
+    err64 = (got.double() - exact).abs().max().item()
+    print(f"C1 fp32 fast: vs fp64 {err64:.2e}")
+    assert err64 <= TOL_FAST_FP32
 
 
 @pytest.mark.parametrize("dtype", list(DTYPES))
@@ -166,7 +187,7 @@ def base_encoder():
     return _encoder_model(12, 768, 12, 3072)
 
 
-def _encoder_errors(base, batch, length, torch_dtype, seed=19):
+def _encoder_errors(base, batch, length, torch_dtype, seed=19, fp32_precision="strict"):
     """(hip vs HF fp32, HF-in-dtype vs HF fp32, hip vs HF-in-dtype) on valid rows."""
 
     from disentangled_flash import enable_deberta_inference
@@ -184,7 +205,8 @@ def _encoder_errors(base, batch, length, torch_dtype, seed=19):
             same = ref(hidden.to(torch_dtype), mask, output_hidden_states=False).last_hidden_state
             del ref
         fast = enable_deberta_inference(copy.deepcopy(base).to("cuda", torch_dtype),
-                                        backend="hip", sequence_lengths=[length])
+                                        backend="hip", sequence_lengths=[length],
+                                        fp32_precision=fp32_precision)
         got = fast.encoder(hidden.to(torch_dtype), mask,
                            output_hidden_states=False).last_hidden_state
         del fast
@@ -219,6 +241,14 @@ def test_12_layer_encoder_matches_huggingface(base_encoder, dtype, shape):
         assert err <= ENCODER_FP32_TOL
     else:
         assert err <= 1.5 * ref_err + TOL[torch_dtype]
+
+
+def test_12_layer_encoder_fast_fp32(base_encoder):
+    """fp32_precision="fast" through the 12-layer encoder, against HF fp32."""
+
+    err, _, _ = _encoder_errors(base_encoder, 8, 256, torch.float32, fp32_precision="fast")
+    print(f"encoder fp32 fast B=8 L=256: hip-vs-HF-fp32 {err:.3e}")
+    assert err <= TOL_FAST_FP32
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
