@@ -137,13 +137,20 @@ def time_p50(fn, steps: int, warmup: int) -> float:
     return statistics.median(samples)
 
 
-def fused_call(inp, has_c2p: bool = True, has_p2c: bool = True, key_splits: int = 0):
+def fused_call(inp, has_c2p: bool = True, has_p2c: bool = True, key_splits: int = 0,
+               strict_fp32: bool = True):
     from disentangled_flash.kernel import deberta_attention_rel
 
     scale_log2 = LOG2E / math.sqrt((1 + int(has_c2p) + int(has_p2c)) * inp["dim"])
     return lambda: deberta_attention_rel(inp["qkv"], inp["pos_key"], inp["pos_query"], inp["lut"],
                                          inp["mask"], inp["heads"], inp["dim"], scale_log2,
-                                         has_c2p, has_p2c, True, key_splits)
+                                         has_c2p, has_p2c, strict_fp32, key_splits)
+
+
+# Kernel dtypes of the edge sweep and the profiling target: "fp32-fast" is fp32
+# data with fp32_precision="fast" (bf16x3 products).
+KERNEL_DTYPES = {**{name: (dtype, True) for name, dtype in DTYPES.items()},
+                 "fp32-fast": (torch.float32, False)}
 
 
 def table_call(inp):
@@ -339,12 +346,12 @@ def bench_edge(steps: int, warmup: int):
     boundary = (1, 63, 64, 65, 127, 129, 383, 384, 511, 512)
     rows = []
     for dim, heads, length in ((128, 8, 512), (32, 16, 384)):
-        for name, dtype in DTYPES.items():
+        for name, (dtype, strict) in KERNEL_DTYPES.items():
             inp = c2_inputs(dtype, padded=True, batch=16, heads=heads, length=length, dim=dim,
                             valid_lengths=boundary)
             for mode, (c2p, p2c) in (("c2p", (True, False)), ("p2c", (False, True)),
                                      ("c2p|p2c", (True, True))):
-                ms = time_launches(fused_call(inp, c2p, p2c), steps, warmup)
+                ms = time_launches(fused_call(inp, c2p, p2c, strict_fp32=strict), steps, warmup)
                 row = {"head_dim": dim, "heads": heads, "batch": 16, "seq_len": length,
                        "dtype": name, "mode": mode, "us": round(ms * 1e3, 1),
                        "tflops_f_attn": round(attention_flops(inp) / ms / 1e9, 1)}
@@ -543,7 +550,7 @@ def main() -> int:
                         help="shape of --kernel-only: c2 (B=32 L=512 H=12 d=64), c5_d32 "
                              "(B=16 L=384 H=16 d=32), c5_d128 (B=16 L=512 H=8 d=128); the C5 "
                              "shapes mix the boundary valid lengths")
-    parser.add_argument("--kernel-dtype", choices=sorted(DTYPES), default="fp16")
+    parser.add_argument("--kernel-dtype", choices=sorted(KERNEL_DTYPES), default="fp16")
     parser.add_argument("--tile-sweep", action="store_true",
                         help="fused op over batch sizes for d=32/64/128 (tile-table evidence)")
     parser.add_argument("--encoder-only", action="store_true",
@@ -603,8 +610,9 @@ def main() -> int:
                           "rows": bench_tile_sweep(args.steps, args.warmup)}), flush=True)
         return 0
     if args.kernel_only:
-        inp = kernel_inputs(args.kernel_shape, DTYPES[args.kernel_dtype])
-        call = fused_call(inp)
+        dtype, strict = KERNEL_DTYPES[args.kernel_dtype]
+        inp = kernel_inputs(args.kernel_shape, dtype)
+        call = fused_call(inp, strict_fp32=strict)
         ramp_clocks(call)
         torch.cuda.synchronize()
         for _ in range(args.steps):

@@ -448,7 +448,10 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   int lutp = 0;                 // next tile's new p2c chunk (pc = wave)
   F crow[C2P ? kSlide : 1][KD];  // rows of this tile's new c2p chunks
   Quad<T> ccar[C2P && kCarry > 0 ? kCarry : 1][kQB];  // c2p values carried into chunks >= kSlide
-  F prow[P2C ? PU : 1][KD];     // rows of this wavefront's p2c chunks wave + 4u
+  QF prow[P2C ? PU : 1][KD];    // rows of this wavefront's p2c chunks wave + 4u
+  // Fast fp32: prow is kept split; the chunk loaded at the end of a tile waits
+  // here (unsplit, its load in flight) until the next tile's p2c products.
+  F prow_in[FAST && P2C ? KD : 1];
 
   // ---- prefetch registers (K, V, mask of the next tile) ----
   u32x4_t pk[NCH];
@@ -501,15 +504,19 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   auto c2p_products = [&]() {
     if constexpr (C2P) {
 #pragma unroll
-      for (int ch = 0; ch < kSlide; ++ch)
+      for (int ch = 0; ch < kSlide; ++ch) {
+        QF cq[KD];
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) cq[kd] = to_q(crow[ch][kd]);
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
           f32x4_t acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int kd = 0; kd < KD; ++kd) acc = M::run(crow[ch][kd], qf[qb][kd], acc);
+          for (int kd = 0; kd < KD; ++kd) acc = M::run(cq[kd], qf[qb][kd], acc);
 #pragma unroll
           for (int r = 0; r < 4; ++r) cnew[ch][qb][r] = static_cast<T>(acc[r]);
         }
+      }
     }
   };
   auto c2p_store = [&]() {
@@ -624,7 +631,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
     for (int u = 0; u < PU; ++u)
 #pragma unroll
-      for (int kd = 0; kd < KD; ++kd) prow[u][kd] = row_frag(rqr, lp[u], kd);
+      for (int kd = 0; kd < KD; ++kd) prow[u][kd] = to_q(row_frag(rqr, lp[u], kd));
   }
 #pragma unroll
   for (int qb = 0; qb < kQB; ++qb) {
@@ -798,6 +805,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
       }
     };
+    if constexpr (FAST && P2C) {
+      if (j0 != jstart) {
+#pragma unroll
+        for (int kd = 0; kd < KD; ++kd) prow[0][kd] = to_q(prow_in[kd]);
+      }
+    }
     if constexpr (D <= 64) {
       switch (wave) {
         case 0: qk_p2c(IntC<0>{}); break;
@@ -839,7 +852,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) prow[u][kd] = prow[u - 1][kd];
 #pragma unroll
-      for (int kd = 0; kd < KD; ++kd) prow[0][kd] = row_frag(rqr, lutp, kd);
+      for (int kd = 0; kd < KD; ++kd) {
+        if constexpr (FAST) {
+          prow_in[kd] = row_frag(rqr, lutp, kd);
+        } else {
+          prow[0][kd] = row_frag(rqr, lutp, kd);
+        }
+      }
       lutp = lut_load(lut_p_index(jn + BN, 0));
     }
     lds_barrier();
