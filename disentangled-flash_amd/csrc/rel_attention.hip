@@ -87,6 +87,7 @@ __device__ inline uint8_t load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 }
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
 
 // Operand traits of the kernel: one k-step is 32 deep, and a lane's operand
@@ -481,10 +482,47 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   //   * one buffer: V of tile n is staged after the first barrier of tile n
   //     (every wavefront has finished PV of tile n-1) and read after the
   //     second, which halves its LDS.
+  // Fast fp32: K and V are staged already split, as a bf16 hi plane followed by
+  // a bf16 lo plane in the same bytes (element e of the fp32 tile at e in each
+  // plane), so each value is split once per workgroup instead of once per
+  // wavefront that reads it; a 16-byte chunk of 4 floats becomes 8 bytes in
+  // each plane.
+  auto split_chunk = [](const u32x4_t& raw, u32x2_t& hi, u32x2_t& lo) {
+    const f32x4_t x = __builtin_bit_cast(f32x4_t, raw);
+    bf16x4_t h, l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = static_cast<__bf16>(x[e]);
+      l[e] = static_cast<__bf16>(x[e] - static_cast<float>(h[e]));
+    }
+    hi = __builtin_bit_cast(u32x2_t, h);
+    lo = __builtin_bit_cast(u32x2_t, l);
+  };
   auto stage_k = [&]() {
 #pragma unroll
     for (int n = 0; n < NCH; ++n)
-      if (NKC >= kThreads || tid < NKC) *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
+      if (NKC >= kThreads || tid < NKC) {
+        if constexpr (FAST) {
+          __bf16* kh = reinterpret_cast<__bf16*>(Ks);
+          u32x2_t hi, lo;
+          split_chunk(pk[n], hi, lo);
+          *reinterpret_cast<u32x2_t*>(kh + kls[n]) = hi;
+          *reinterpret_cast<u32x2_t*>(kh + BN * LY::KS_LD + kls[n]) = lo;
+        } else {
+          *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
+        }
+      }
+  };
+  // Fast fp32: K fragment of key row `row`, k-step kd, from the split planes.
+  auto k_read = [&](int row, int kd) -> QF {
+    if constexpr (FAST) {
+      const int off = row * LY::KS_LD + 32 * kd + 8 * g;
+      const __bf16* kh = reinterpret_cast<const __bf16*>(Ks);
+      return QF{*reinterpret_cast<const bf16x8_t*>(kh + off),
+                *reinterpret_cast<const bf16x8_t*>(kh + BN * LY::KS_LD + off)};
+    } else {
+      return QF{};  // not used by the other instances
+    }
   };
   // V rows of 16-bit T are 8-byte aligned only (VS_LD = D + 4): two 8-byte
   // stores per chunk (half a chunk = E16 / 2 elements each).
@@ -492,8 +530,16 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
     for (int n = 0; n < NVB; ++n)
       if (NKC >= kThreads || tid < NKC) {
-        *reinterpret_cast<u32x2_t*>(vs + vls[n]) = u32x2_t{pv[n][0], pv[n][1]};
-        *reinterpret_cast<u32x2_t*>(vs + vls[n] + E16 / 2) = u32x2_t{pv[n][2], pv[n][3]};
+        if constexpr (FAST) {
+          __bf16* vh = reinterpret_cast<__bf16*>(vs);
+          u32x2_t hi, lo;
+          split_chunk(pv[n], hi, lo);
+          *reinterpret_cast<u32x2_t*>(vh + vls[n]) = hi;
+          *reinterpret_cast<u32x2_t*>(vh + BN * LY::VS_LD + vls[n]) = lo;
+        } else {
+          *reinterpret_cast<u32x2_t*>(vs + vls[n]) = u32x2_t{pv[n][0], pv[n][1]};
+          *reinterpret_cast<u32x2_t*>(vs + vls[n] + E16 / 2) = u32x2_t{pv[n][2], pv[n][3]};
+        }
       }
   };
 
@@ -503,19 +549,33 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   Quad<T> cnew[C2P ? kSlide : 1][kQB];
   auto c2p_products = [&]() {
     if constexpr (C2P) {
+      if constexpr (FAST) {
+        // Each row fragment split once for its kQB products.
 #pragma unroll
-      for (int ch = 0; ch < kSlide; ++ch) {
-        QF cq[KD];
+        for (int ch = 0; ch < kSlide; ++ch) {
+          QF cq[KD];
 #pragma unroll
-        for (int kd = 0; kd < KD; ++kd) cq[kd] = to_q(crow[ch][kd]);
+          for (int kd = 0; kd < KD; ++kd) cq[kd] = to_q(crow[ch][kd]);
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) {
-          f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+          for (int qb = 0; qb < kQB; ++qb) {
+            f32x4_t acc{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int kd = 0; kd < KD; ++kd) acc = M::run(cq[kd], qf[qb][kd], acc);
+            for (int kd = 0; kd < KD; ++kd) acc = M::run(cq[kd], qf[qb][kd], acc);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) cnew[ch][qb][r] = static_cast<T>(acc[r]);
+            for (int r = 0; r < 4; ++r) cnew[ch][qb][r] = static_cast<T>(acc[r]);
+          }
         }
+      } else {
+#pragma unroll
+        for (int ch = 0; ch < kSlide; ++ch)
+#pragma unroll
+          for (int qb = 0; qb < kQB; ++qb) {
+            f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kd = 0; kd < KD; ++kd) acc = M::run(crow[ch][kd], qf[qb][kd], acc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cnew[ch][qb][r] = static_cast<T>(acc[r]);
+          }
       }
     }
   };
@@ -769,19 +829,29 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       constexpr int W = decltype(wave_c)::value;
       // K fragments one key block ahead (two register sets), so that the
       // reads of block kb + 1 are in flight during the MFMAs of block kb.
-      F kfa[2][KD];
+      QF kfa[2][KD];
 #pragma unroll
-      for (int kd = 0; kd < KD; ++kd)
-        kfa[0][kd] = *reinterpret_cast<const F*>(Ks + key_of(c) * LY::KS_LD + 32 * kd + 8 * g);
+      for (int kd = 0; kd < KD; ++kd) {
+        if constexpr (FAST) {
+          kfa[0][kd] = k_read(key_of(c), kd);
+        } else {
+          kfa[0][kd] = *reinterpret_cast<const F*>(Ks + key_of(c) * LY::KS_LD + 32 * kd + 8 * g);
+        }
+      }
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         QF kf[KD];
 #pragma unroll
-        for (int kd = 0; kd < KD; ++kd) kf[kd] = to_q(kfa[kb & 1][kd]);
+        for (int kd = 0; kd < KD; ++kd) kf[kd] = kfa[kb & 1][kd];
         if (kb + 1 < KB) {
 #pragma unroll
-          for (int kd = 0; kd < KD; ++kd)
-            kfa[(kb + 1) & 1][kd] = *reinterpret_cast<const F*>(Ks + (16 * (kb + 1) + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+          for (int kd = 0; kd < KD; ++kd) {
+            if constexpr (FAST) {
+              kfa[(kb + 1) & 1][kd] = k_read(16 * (kb + 1) + key_of(c), kd);
+            } else {
+              kfa[(kb + 1) & 1][kd] = *reinterpret_cast<const F*>(Ks + (16 * (kb + 1) + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+            }
+          }
         }
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
@@ -823,8 +893,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       for (int kb = 0; kb < KB; ++kb) {
         QF kf[KD];
 #pragma unroll
-        for (int kd = 0; kd < KD; ++kd)
-          kf[kd] = to_q(*reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g));
+        for (int kd = 0; kd < KD; ++kd) {
+          if constexpr (FAST) {
+            kf[kd] = k_read(16 * kb + key_of(c), kd);
+          } else {
+            kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+          }
+        }
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) {
           f32x4_t acc{0.f, 0.f, 0.f, 0.f};
@@ -946,8 +1021,26 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     // latency hides under it (93.9 -> 89.3 us on the C5 shape); with one term,
     // or for d <= 64, that cost more registers than it saved (+2-5 %), and they
     // are read next to their MFMAs.
-    auto vt_frag = [&](int ks, int db) {
-      if constexpr (sizeof(T) == 4) {
+    // Fast fp32: the transposing read of the 16-bit path (below) on one plane
+    // of the split V tile.
+    auto vt_tr16 = [&](const void* tile, int ks, int db) -> u32x4_t {
+      const uint16_t* base = static_cast<const uint16_t*>(tile);
+      const uint16_t* p_lo = base + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
+      const uint16_t* p_hi = p_lo + 16 * LY::VS_LD;
+      const u32x2_t lo = __builtin_bit_cast(
+          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
+      const u32x2_t hi = __builtin_bit_cast(
+          u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
+      return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+    };
+    auto vt_frag = [&](int ks, int db) -> QF {
+      if constexpr (FAST) {
+        // The P^T key order of the 16-bit path is the fp32 one (below), so the
+        // transposing reads of the two planes give the split operand directly.
+        const __bf16* vh = reinterpret_cast<const __bf16*>(vt_cur);
+        return QF{__builtin_bit_cast(bf16x8_t, vt_tr16(vh, ks, db)),
+                  __builtin_bit_cast(bf16x8_t, vt_tr16(vh + BN * LY::VS_LD, ks, db))};
+      } else if constexpr (sizeof(T) == 4) {
         // fp32: element e holds V[key][16db + c] for the keys of the P^T
         // operand, 32ks + g + 4e (e < 4) and 32ks + 16 + g + 4(e - 4).
         F a;
@@ -972,7 +1065,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       }
     };
     constexpr bool kVtEarly = D >= 128 && !SPLIT && C2P && P2C;
-    F vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
+    QF vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
     if constexpr (kVtEarly) {
 #pragma unroll
       for (int ks = 0; ks < BN / 32; ++ks)
@@ -1048,20 +1141,34 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           rs[qb] = M::run(ones, pf[qb], rs[qb]);
         }
       }
-      QF pq[kQB];
+      if constexpr (FAST) {
+        // P split once for its DB products; V^T comes split from the planes.
+        QF pq[kQB];
 #pragma unroll
-      for (int qb = 0; qb < kQB; ++qb) pq[qb] = to_q(pf[qb]);
+        for (int qb = 0; qb < kQB; ++qb) pq[qb] = to_q(pf[qb]);
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        F a;
-        if constexpr (kVtEarly) {
-          a = vt_all[ks][db];
-        } else {
-          a = vt_frag(ks, db);
+        for (int db = 0; db < DB; ++db) {
+          QF a;
+          if constexpr (kVtEarly) {
+            a = vt_all[ks][db];
+          } else {
+            a = vt_frag(ks, db);
+          }
+#pragma unroll
+          for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pq[qb], o[db][qb]);
         }
-        const QF aq = to_q(a);
+      } else {
 #pragma unroll
-        for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(aq, pq[qb], o[db][qb]);
+        for (int db = 0; db < DB; ++db) {
+          F a;
+          if constexpr (kVtEarly) {
+            a = vt_all[ks][db];
+          } else {
+            a = vt_frag(ks, db);
+          }
+#pragma unroll
+          for (int qb = 0; qb < kQB; ++qb) o[db][qb] = M::run(a, pf[qb], o[db][qb]);
+        }
       }
     }
 
