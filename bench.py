@@ -245,9 +245,33 @@ def encoder_inputs(batch: int, length: int, dtype, device, seed: int = 19):
     return hidden, mask.to(device=device, dtype=torch.long)
 
 
+def _sig(v, digits: int = 4):
+    """Floats to ``digits`` significant digits for the JSON line (errors are ~1e-6)."""
+
+    return float(f"{v:.{digits}g}") if isinstance(v, float) else v
+
+
+def forward_peak_bytes(run) -> int:
+    """Peak bytes a forward allocates on top of what is resident before it."""
+
+    torch.cuda.synchronize()
+    resident = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    run()
+    torch.cuda.synchronize()
+    return torch.cuda.max_memory_allocated() - resident
+
+
 def bench_encoder(batch: int, length: int, steps: int, warmup: int,
-                  backends=("original", "optimized", "hip")):
-    """12-layer encoder latency: HF original vs torch ``optimized`` vs ``hip``."""
+                  backends=("original", "optimized", "hip"), dtype=torch.float16,
+                  fp32_precision: str = "strict"):
+    """12-layer encoder latency: HF original vs torch ``optimized`` vs ``hip``.
+
+    ``<backend>_peak_gb`` is the reference's peak-memory figure for one model
+    (``benchmark_cuda.py:548-551`` resets the peak counter before its measured
+    calls): the encoder's parameters, the inputs and the forward's peak
+    allocation on top of them.
+    """
 
     import copy
 
@@ -256,23 +280,30 @@ def bench_encoder(batch: int, length: int, steps: int, warmup: int,
     from disentangled_flash import enable_deberta_inference
 
     torch.manual_seed(17)
-    base = DebertaV2Model(encoder_config()).to("cuda", torch.float16).eval()
-    hidden, mask = encoder_inputs(batch, length, torch.float16, "cuda")
+    base = DebertaV2Model(encoder_config()).to("cuda", dtype).eval()
+    hidden, mask = encoder_inputs(batch, length, dtype, "cuda")
+    weights = sum(t.numel() * t.element_size()
+                  for t in list(base.encoder.parameters()) + list(base.encoder.buffers()))
+    resident = weights + hidden.numel() * hidden.element_size() + mask.numel() * mask.element_size()
     results = {}
     with torch.inference_mode():
         original = base.encoder
+        original_run = lambda: original(hidden, mask, output_hidden_states=False)  # noqa: E731
         if "original" in backends:
-            results["original_ms"] = time_p50(
-                lambda: original(hidden, mask, output_hidden_states=False), steps, warmup)
-        reference_out = original(hidden, mask, output_hidden_states=False).last_hidden_state
+            results["original_ms"] = time_p50(original_run, steps, warmup)
+            results["original_peak_gb"] = round(
+                (resident + forward_peak_bytes(original_run)) / 1e9, 3)
+        reference_out = original_run().last_hidden_state
         for backend in (b for b in ("optimized", "hip") if b in backends):
             model = copy.deepcopy(base)
-            enable_deberta_inference(model, backend=backend, sequence_lengths=[length])
+            enable_deberta_inference(model, backend=backend, sequence_lengths=[length],
+                                     fp32_precision=fp32_precision)
             encoder = model.encoder
             plans = encoder.active_plans
             run = lambda: encoder.forward_prepared(hidden, mask, plans,  # noqa: E731
                                                    output_hidden_states=False)
             results[f"{backend}_ms"] = time_p50(run, steps, warmup)
+            results[f"{backend}_peak_gb"] = round((resident + forward_peak_bytes(run)) / 1e9, 3)
             out = run().last_hidden_state
             results[f"{backend}_max_abs_err_vs_original"] = float(
                 (out.float() - reference_out.float()).abs().max())
@@ -692,9 +723,20 @@ def main() -> int:
     if not args.skip_encoder:
         enc = bench_encoder(32, 512, args.encoder_steps, 3)
         line["encoder"] = {"batch": 32, "seq_len": 512, "layers": 12, "dtype": "fp16",
-                           **{k: (round(v, 4) if isinstance(v, float) else v)
-                              for k, v in enc.items()}}
+                           **{k: _sig(v) for k, v in enc.items()}}
         log(f"encoder: {enc}")
+        # fp32 at the same shape (the reference publishes its fp32 encoder latency
+        # there, README.md:210): strict and the bf16x3 fast mode, a few forwards each.
+        enc32 = bench_encoder(32, 512, 5, 2, dtype=torch.float32)
+        fast32 = bench_encoder(32, 512, 5, 2, backends=("hip",), dtype=torch.float32,
+                               fp32_precision="fast")
+        line["encoder"]["fp32"] = {
+            **{k: _sig(v) for k, v in enc32.items()},
+            "hip_fast_ms": _sig(fast32["hip_ms"]),
+            "hip_fast_peak_gb": _sig(fast32["hip_peak_gb"]),
+            "hip_fast_max_abs_err_vs_original": _sig(fast32["hip_max_abs_err_vs_original"]),
+        }
+        log(f"encoder fp32: {line['encoder']['fp32']}")
     if not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline()
         log(f"cpu baseline: {line['cpu_baseline']}")
