@@ -197,3 +197,28 @@ def test_optimized_restatement_matches_original(name):
 def test_spec_defaults():
     spec = AttentionSpec(hidden_size=768, num_heads=12, head_dim=64)
     assert spec.span == 256 and spec.scale_factor == 3
+
+
+def test_float64_buckets_differ_from_float32_somewhere():
+    """Why the position plan stays on the host, as in the reference (``position.py:104-110``).
+
+    The reference buckets deltas with a float32 log on the CPU.  A float64 (or
+    device) log gives another bucket where ``log(|d| / mid) / log((max - 1) / mid) * (mid - 1)``
+    lies within float32 rounding of an integer: at buckets 256 / max_position 256,
+    |d| = 1292 is bucket 555 in exact arithmetic and 554 in the reference's float32.
+    For the encoder configurations here (256 buckets, max_position 512) the two agree.
+    """
+
+    from disentangled_flash.modeling import make_log_bucket_position
+
+    deltas = np.array([-1292, 1292], dtype=np.int64)
+    exact = np.array([log_bucket_scalar(int(d), 256, 256) for d in deltas])
+    assert list(exact) == [-555, 555]
+    assert list(log_bucket(deltas, 256, 256, dtype=np.float64)) == [-555, 555]
+    ref = make_log_bucket_position(torch.from_numpy(deltas), 256, 256).to(torch.long).numpy()
+    assert list(ref) == [-554, 554]
+    assert list(log_bucket(deltas, 256, 256)) == [-554, 554]  # the float32 restatement agrees
+
+    span = np.arange(-8191, 8192)
+    ref = make_log_bucket_position(torch.from_numpy(span), 256, 512).to(torch.long).numpy()
+    assert np.array_equal(ref, log_bucket(span, 256, 512, dtype=np.float64))
