@@ -243,6 +243,19 @@ def test_12_layer_encoder_matches_huggingface(base_encoder, dtype, shape):
         assert err <= 1.5 * ref_err + TOL[torch_dtype]
 
 
+@pytest.mark.parametrize("shape", [(1, 16), (16, 64), (32, 128), (8, 384), (1, 512)],
+                         ids=lambda s: f"b{s[0]}_l{s[1]}")
+def test_c3_sweep_cells_fp16(base_encoder, shape):
+    """More cells of the C3 sweep (B x L) in fp16: tiny buckets, mid sizes, and B=1 at
+    L=512, where the attention runs its split-key form."""
+
+    batch, length = shape
+    err, ref_err, err_same = _encoder_errors(base_encoder, batch, length, torch.float16, seed=batch + length)
+    print(f"encoder fp16 B={batch} L={length}: hip-vs-HF-fp32 {err:.3e}, "
+          f"HF-fp16-vs-HF-fp32 {ref_err:.3e}, hip-vs-HF-fp16 {err_same:.3e}")
+    assert err <= 1.5 * ref_err + TOL[torch.float16]
+
+
 def test_12_layer_encoder_fast_fp32(base_encoder):
     """fp32_precision="fast" through the 12-layer encoder, against HF fp32."""
 
