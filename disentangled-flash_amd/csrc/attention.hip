@@ -561,7 +561,11 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
   if ((has_c2p && !pos_key) || (has_p2c && !pos_query)) return DFLASH_ERR_NULL;
   const int esize = dtype == DFLASH_DTYPE_FP32 ? 4 : 2;
   if (stride_l < D || stride_b < 1 || stride_h < 1) return DFLASH_ERR_SHAPE;
-  if (static_cast<int64_t>(L) * stride_l >= (int64_t{1} << 31)) return DFLASH_ERR_TOO_LARGE;
+  // The kernel addresses one (b, h) slice of Q/K/V and the relative rows through
+  // 32-bit byte offsets of buffer resources: both must stay below 2^31 bytes.
+  if (static_cast<int64_t>(L) * stride_l * esize >= (int64_t{1} << 31) ||
+      static_cast<int64_t>(S) * D * esize >= (int64_t{1} << 31))
+    return DFLASH_ERR_TOO_LARGE;
   if (((stride_b | stride_h | stride_l) * esize) % 16 != 0) return DFLASH_ERR_ALIGN;
   const uintptr_t addr_or = reinterpret_cast<uintptr_t>(query) |
                             reinterpret_cast<uintptr_t>(key) |

@@ -312,6 +312,12 @@ def test_c_abi_rejects_bad_arguments():
                                   1, 0, 0, 1, None)
     assert rc == -1
     assert b"head dimension" in lib.dflash_error_string(-3)
+    # A (b, h) slice past 2^31 bytes (fp32: 4-byte elements) is refused before any launch.
+    lut = torch.zeros(16, device="cuda", dtype=torch.int32)
+    rc = lib.dflash_attention_rel_fwd(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 64, 1 << 16,
+                                      x.data_ptr(), x.data_ptr(), lut.data_ptr(), x.data_ptr(),
+                                      x.data_ptr(), 1, 1, 1 << 13, 64, 8, 1.0, 1, 1, 2, 1, None)
+    assert rc == -6
 
 
 def test_empty_batch_is_a_no_op():
