@@ -96,8 +96,8 @@ DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const vo
  *                       and the product runs as three bf16 MFMAs (relative error
  *                       about 2^-16 per product, below TF32's 2^-11).
  * B == 0 is a no-op that returns 0 (pointers are not inspected).
- * DFLASH_ERR_TOO_LARGE when one (b, h) slice spans 2^31 bytes or more
- * ((L - 1) * stride_l + D elements) or the relative rows of a head do (S * D).
+ * DFLASH_ERR_TOO_LARGE when L * stride_l elements or the S * D elements of one
+ * head's relative rows reach 2^31 bytes (the kernel's 32-bit buffer offsets).
  */
 DFLASH_API int dflash_attention_rel_fwd(const void* query, const void* key, const void* value,
                              int64_t stride_b, int64_t stride_h, int64_t stride_l,
