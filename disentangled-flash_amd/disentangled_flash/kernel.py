@@ -339,8 +339,9 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
     def _fused_projection(self, hidden_states: torch.Tensor) -> torch.Tensor:
         """Fused QKV projection ``[B, L, 3*H*d]`` (``_torch.py:284-297``).
 
-        fp16/bf16 projections of a supported width run on the hand-written gfx950
-        GEMM (``dflash_linear_fwd``); others on ``F.linear``.
+        fp16/bf16 projections of a supported width and at least
+        ``layers.HIP_GEMM_MIN_ROWS`` rows run on the hand-written gfx950 GEMM
+        (``dflash_linear_fwd``); others on ``F.linear``.
         """
 
         prep = self._prepared
@@ -349,6 +350,7 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
                 "fused QKV projection is not prepared; call prepare_for_inference() first"
             )
         if layers.USE_HIP_GEMM and hidden_states.device.type == "cuda" \
+                and layers.hip_gemm_rows(hidden_states) \
                 and gemm_fits(prep.qkv_weight, prep.qkv_bias) \
                 and hidden_states.dtype == prep.qkv_weight.dtype:
             return linear_epilogue(gemm_rows(hidden_states), prep.qkv_weight, prep.qkv_bias, None,

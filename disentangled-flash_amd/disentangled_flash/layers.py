@@ -83,6 +83,22 @@ def _layernorm_fake(x, weight, bias, eps):
 # an encoder is prepared and on every QKV projection.  A switch for A/B timing.
 USE_HIP_GEMM = True
 
+# Fewest rows (tokens, M = B*L) of a call for which the encoder projections run
+# on the hand-written GEMM.  Its 256-row tiles leave most CUs idle at a few
+# thousand rows; measured as HIP-graph replays of whole encoders (12-layer base
+# fp16, 24-layer xlarge bf16), hipBLASLt plus a separate GELU is faster at every
+# smaller row count (up to 1.5x at 512 rows) and the two tie at 16384 rows.
+# Checked on every call: the encoder's layer program binds the fused steps once
+# per bucket, while B varies per call.
+HIP_GEMM_MIN_ROWS = 16384
+
+
+def hip_gemm_rows(x: torch.Tensor) -> bool:
+    """True if ``x`` (``[..., K]``) has enough rows for the hand-written GEMM."""
+
+    k = x.shape[-1]
+    return k > 0 and x.numel() // k >= HIP_GEMM_MIN_ROWS
+
 # dflash_linear_fwd epilogues.
 GEMM_BIAS = 0
 GEMM_BIAS_GELU = 1
@@ -169,8 +185,11 @@ def fusable_intermediate(module: nn.Module) -> bool:
 
 
 def intermediate_block(module: nn.Module, hidden_states: torch.Tensor) -> torch.Tensor:
-    """``module(hidden_states)`` as one GEMM with the GELU in its epilogue."""
+    """``module(hidden_states)`` as one GEMM with the GELU in its epilogue (at
+    :data:`HIP_GEMM_MIN_ROWS` rows or more; below, the module itself)."""
 
+    if not hip_gemm_rows(hidden_states):
+        return module(hidden_states)
     return linear_epilogue(gemm_rows(hidden_states), module.dense.weight, module.dense.bias,
                            None, GEMM_BIAS_GELU)
 
@@ -178,8 +197,11 @@ def intermediate_block(module: nn.Module, hidden_states: torch.Tensor) -> torch.
 def output_block_gemm(module: nn.Module, hidden_states: torch.Tensor,
                       input_tensor: torch.Tensor) -> torch.Tensor:
     """``module(hidden_states, input_tensor)``: GEMM with the residual added in its
-    epilogue, then LayerNorm over the sum (one read of it instead of two)."""
+    epilogue, then LayerNorm over the sum (one read of it instead of two).  Below
+    :data:`HIP_GEMM_MIN_ROWS` rows: hipBLASLt and the fused add + LayerNorm."""
 
+    if not hip_gemm_rows(hidden_states):
+        return output_block(module, hidden_states, input_tensor)
     summed = linear_epilogue(gemm_rows(hidden_states), module.dense.weight, module.dense.bias,
                              gemm_rows(input_tensor), GEMM_BIAS_ADD)
     norm = module.LayerNorm

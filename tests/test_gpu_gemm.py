@@ -118,9 +118,10 @@ def test_linear_ops_and_errors():
     assert lib.dflash_linear_fwd(None, None, None, None, None, 0, 192, 32, 0, 0, None) == 0
 
 
-def test_encoder_gemm_tails_match_modules():
+def test_encoder_gemm_tails_match_modules(monkeypatch):
     """The fused tails against the HF module pieces they replace, in fp16."""
 
+    from disentangled_flash import layers
     from disentangled_flash.layers import (
         fusable_intermediate,
         intermediate_block,
@@ -132,6 +133,7 @@ def test_encoder_gemm_tails_match_modules():
         DebertaV2SelfOutput,
     )
 
+    monkeypatch.setattr(layers, "HIP_GEMM_MIN_ROWS", 0)  # the hand-written GEMM at 520 rows
     cfg = DebertaV2Config(hidden_size=768, intermediate_size=3072, hidden_act="gelu",
                           hidden_dropout_prob=0.0, layer_norm_eps=1e-7)
     torch.manual_seed(3)

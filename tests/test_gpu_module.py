@@ -278,6 +278,21 @@ def test_encoder_with_library_projections(base_encoder, dtype, monkeypatch):
     assert err <= 1.5 * ref_err + TOL[torch_dtype]
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_encoder_with_hand_written_gemm_below_the_row_threshold(base_encoder, dtype, monkeypatch):
+    """The hand-written GEMM (fused QKV, GELU and residual epilogues) in every layer at a
+    bucket below ``HIP_GEMM_MIN_ROWS``, where the encoder would otherwise use hipBLASLt."""
+
+    from disentangled_flash import layers
+
+    monkeypatch.setattr(layers, "HIP_GEMM_MIN_ROWS", 0)
+    torch_dtype = DTYPES[dtype]
+    err, ref_err, err_same = _encoder_errors(base_encoder, 8, 256, torch_dtype)
+    print(f"encoder (hand-written GEMM at 2048 rows) {dtype}: hip-vs-HF-fp32 {err:.3e}, "
+          f"HF-{dtype}-vs-HF-fp32 {ref_err:.3e}")
+    assert err <= 1.5 * ref_err + TOL[torch_dtype]
+
+
 def test_xlarge_bf16_buckets():
     """C4: the full 24-layer xlarge-shaped encoder (hidden 1536, 24 heads, FFN 6144), bf16,
     B=8, log-normal lengths (median 60) clipped to [16, bucket], buckets 64/128/256."""
