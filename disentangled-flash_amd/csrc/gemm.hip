@@ -49,7 +49,6 @@ namespace {
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int kGemmThreads = 256;  // 4 wavefronts, 2 x 2 over the tile
-constexpr int kBM = 256;           // rows of Y per workgroup
 constexpr int kBK = 32;            // K per stage (one MFMA k-step)
 
 constexpr int kEpiBias = 0;
@@ -119,32 +118,33 @@ __device__ inline void wait_vmem() {
 }  // namespace
 
 // Tile configuration: a workgroup of WAVES_M x WAVES_N wavefronts computes a
-// kBM x BN tile of Y (wavefront tile kBM/WAVES_M x BN/WAVES_N) through a ring of
+// BM x BN tile of Y (wavefront tile BM/WAVES_M x BN/WAVES_N) through a ring of
 // STAGES LDS stages; WGS workgroups per CU are budgeted for.
-template <int BN_, int STAGES_, int WGS_, int WAVES_M_, int WAVES_N_>
+template <int BN_, int STAGES_, int WGS_, int WAVES_M_, int WAVES_N_, int BM_ = 256>
 struct GemmConfig {
+  static constexpr int BM = BM_;
   static constexpr int BN = BN_;
   static constexpr int STAGES = STAGES_;
   static constexpr int WGS = WGS_;
   static constexpr int WAVES_M = WAVES_M_;
   static constexpr int WAVES_N = WAVES_N_;
   static constexpr int THREADS = 64 * WAVES_M * WAVES_N;
-  static constexpr int WM = kBM / WAVES_M;
+  static constexpr int WM = BM / WAVES_M;
   static constexpr int WN = BN / WAVES_N;
   static constexpr int MB = WM / 16;                 // 16-row blocks per wavefront
   static constexpr int NB = WN / 16;                 // 16-column blocks per wavefront
-  static constexpr int A_CHUNKS = kBM * kBK / 8;     // 16-byte chunks of a stage's X tile
+  static constexpr int A_CHUNKS = BM * kBK / 8;      // 16-byte chunks of a stage's X tile
   static constexpr int B_CHUNKS = BN * kBK / 8;
   // Copy instructions per thread per stage.  A chunk count that is not a
   // multiple of the workgroup size leaves the last round to the first
   // wavefronts (whole wavefronts, so the counts stay wavefront-uniform).
   static constexpr int A_LOADS = (A_CHUNKS + THREADS - 1) / THREADS;
   static constexpr int B_LOADS = (B_CHUNKS + THREADS - 1) / THREADS;
-  static constexpr int A_BYTES = kBM * kBK * 2;
-  static constexpr int STAGE_BYTES = (kBM + BN) * kBK * 2;
+  static constexpr int A_BYTES = BM * kBK * 2;
+  static constexpr int STAGE_BYTES = (BM + BN) * kBK * 2;
   static constexpr int TILE_LD = BN + 8;             // epilogue staging row (elements)
   static constexpr int RING = STAGES * STAGE_BYTES;
-  static constexpr int STAGING = kBM * TILE_LD * 2;
+  static constexpr int STAGING = BM * TILE_LD * 2;
   static constexpr int LDS = RING > STAGING ? RING : STAGING;
   static_assert(A_CHUNKS % 64 == 0 && B_CHUNKS % 64 == 0, "copies in whole wavefronts");
   static_assert(WM % 16 == 0 && WN % 16 == 0, "wavefront tile of whole MFMA blocks");
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(CF::THREADS, CF::WGS) void gemm_kernel(GemmArgs a) 
   if (t >= total) return;  // padding of the grid to a multiple of 8
   const int mb = t / a.n_blocks;
   const int nb = t - mb * a.n_blocks;
-  const int m_base = mb * kBM;
+  const int m_base = mb * CF::BM;
   const int n_base = nb * BN;
   const int K = a.K;
 
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(CF::THREADS, CF::WGS) void gemm_kernel(GemmArgs a) 
   typedef T Oct __attribute__((ext_vector_type(8)));
   const T* res = reinterpret_cast<const T*>(a.residual);
   T* Y = reinterpret_cast<T*>(a.y);
-  const int rows = min(kBM, a.M - m_base);
+  const int rows = min(CF::BM, a.M - m_base);
   for (int q = tid; q < rows * kRowChunks; q += NT) {
     const int row = q / kRowChunks;
     const int ch = q - row * kRowChunks;
@@ -376,10 +376,14 @@ __global__ __launch_bounds__(CF::THREADS, CF::WGS) void gemm_kernel(GemmArgs a) 
 namespace {
 
 // Configurations: 256 x 192 tiles at one workgroup per CU (N % 192 == 0) and
-// 256 x 128 tiles at two (N % 128 == 0).
+// 256 x 128 tiles at two (N % 128 == 0); for few rows, 64 x 128 tiles at three
+// workgroups per CU and 64 x 64 tiles at four, which give four times the tiles
+// of the 256-row forms (at 512 rows a 1536-wide projection has 96 and 192).
 using CfgWide = GemmConfig<192, 5, 1, 2, 2>;
 using CfgPair = GemmConfig<128, 3, 2, 2, 2>;
 using CfgEight = GemmConfig<192, 5, 1, 4, 2>;
+using CfgSmall = GemmConfig<128, 4, 3, 2, 2, 64>;
+using CfgTiny = GemmConfig<64, 4, 4, 2, 2, 64>;
 
 template <typename T, int EPI, typename CF>
 int launch_gemm(GemmArgs args, hipStream_t stream) {
@@ -396,6 +400,7 @@ int launch_gemm(GemmArgs args, hipStream_t stream) {
     if (err == hipSuccess && bit != 0) raised.fetch_or(bit, std::memory_order_release);
   }
   if (err != hipSuccess) return static_cast<int>(err);
+  args.m_blocks = (args.M + CF::BM - 1) / CF::BM;
   args.n_blocks = args.N / CF::BN;
   const int64_t tiles = static_cast<int64_t>(args.m_blocks) * args.n_blocks;
   const int64_t grid = ((tiles + 7) / 8) * 8;
@@ -405,7 +410,8 @@ int launch_gemm(GemmArgs args, hipStream_t stream) {
   return static_cast<int>(hipGetLastError());
 }
 
-// config: 0 = automatic, 1 = CfgWide, 2 = CfgPair, 3 = CfgEight.  Automatic
+// config: 0 = automatic, 1 = CfgWide, 2 = CfgPair, 3 = CfgEight, 4 = CfgSmall,
+// 5 = CfgTiny.  Automatic
 // (measured at M = 16384, fp16): CfgEight where N % 192 == 0 (QKV 71.7 us,
 // hidden-wide dense 24.5 us), except the GELU epilogue, whose VALU work
 // overlaps better at two workgroups per CU (CfgPair, FFN intermediate 108.5
@@ -422,6 +428,10 @@ int pick_config(const GemmArgs& args, int config, hipStream_t stream) {
       return pair_ok ? launch_gemm<T, EPI, CfgPair>(args, stream) : DFLASH_ERR_SHAPE;
     case 3:
       return wide_ok ? launch_gemm<T, EPI, CfgEight>(args, stream) : DFLASH_ERR_SHAPE;
+    case 4:
+      return pair_ok ? launch_gemm<T, EPI, CfgSmall>(args, stream) : DFLASH_ERR_SHAPE;
+    case 5:
+      return launch_gemm<T, EPI, CfgTiny>(args, stream);  // N % 64 == 0 is checked on entry
     default:
       return DFLASH_ERR_SHAPE;
   }
@@ -465,7 +475,7 @@ extern "C" int dflash_linear_fwd(const void* x, const void* weight, const void* 
   // Bits 8.. of `epilogue` select a tile configuration (0 = automatic).
   const int config = epilogue >> 8;
   epilogue &= 0xff;
-  GemmArgs args{x, weight, bias, residual, y, M, N, K, (M + kBM - 1) / kBM, 0};
+  GemmArgs args{x, weight, bias, residual, y, M, N, K, 0, 0};
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == DFLASH_DTYPE_FP16) return dispatch_epilogue<_Float16>(args, epilogue, config, s);
   if (dtype == DFLASH_DTYPE_BF16) return dispatch_epilogue<__bf16>(args, epilogue, config, s);

@@ -99,6 +99,10 @@ def hip_gemm_rows(x: torch.Tensor) -> bool:
     k = x.shape[-1]
     return k > 0 and x.numel() // k >= HIP_GEMM_MIN_ROWS
 
+# Tile configuration the encoder asks dflash_linear_fwd for (bits 8.. of its
+# epilogue argument; 0 = the library's choice by shape).  A switch for A/B timing.
+GEMM_CONFIG = 0
+
 # dflash_linear_fwd epilogues.
 GEMM_BIAS = 0
 GEMM_BIAS_GELU = 1
@@ -127,7 +131,8 @@ def linear_epilogue(
     code = lib.dflash_linear_fwd(
         x.data_ptr(), weight.data_ptr(), bias.data_ptr(),
         residual.data_ptr() if residual is not None else None, out.data_ptr(), rows, n, k,
-        int(epilogue), _lib.DTYPE_CODES[x.dtype], _lib.current_stream_handle(x.device))
+        int(epilogue) | (int(GEMM_CONFIG) << 8), _lib.DTYPE_CODES[x.dtype],
+        _lib.current_stream_handle(x.device))
     _lib.check(code, "dflash_linear_fwd")
     return out
 
