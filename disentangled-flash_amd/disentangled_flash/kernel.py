@@ -339,9 +339,9 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
     def _fused_projection(self, hidden_states: torch.Tensor) -> torch.Tensor:
         """Fused QKV projection ``[B, L, 3*H*d]`` (``_torch.py:284-297``).
 
-        fp16/bf16 projections of a supported width and at least
-        ``layers.HIP_GEMM_MIN_ROWS`` rows run on the hand-written gfx950 GEMM
-        (``dflash_linear_fwd``); others on ``F.linear``.
+        fp16/bf16 projections of a supported width run on the hand-written gfx950
+        GEMM (``dflash_linear_fwd``) where ``layers.hip_gemm_rows`` says so (by
+        row count and launch mode); others on ``F.linear``.
         """
 
         prep = self._prepared

@@ -20,6 +20,8 @@ traces through them, like the attention ops.
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 from torch import nn
 from torch.nn import functional as F
@@ -83,21 +85,53 @@ def _layernorm_fake(x, weight, bias, eps):
 # an encoder is prepared and on every QKV projection.  A switch for A/B timing.
 USE_HIP_GEMM = True
 
-# Fewest rows (tokens, M = B*L) of a call for which the encoder projections run
-# on the hand-written GEMM.  Its 256-row tiles leave most CUs idle at a few
-# thousand rows; measured as HIP-graph replays of whole encoders (12-layer base
-# fp16, 24-layer xlarge bf16), hipBLASLt plus a separate GELU is faster at every
-# smaller row count (up to 1.5x at 512 rows) and the two tie at 16384 rows.
-# Checked on every call: the encoder's layer program binds the fused steps once
-# per bucket, while B varies per call.
+# Fewest rows (tokens, M = B*L) for which the encoder projections always run on
+# the hand-written GEMM.  Measured on whole encoders (12-layer base fp16, 24-layer
+# xlarge bf16), below it the choice depends on how the forward is launched:
+#   * HIP-graph replay: hipBLASLt plus a separate GELU is faster on the device (up
+#     to 1.5x at 512 rows: the GEMM's 256-row tiles leave most CUs idle);
+#   * eager, hidden 768 (K = 768): a forward at a few thousand rows is bound by
+#     launch time, and an F.linear call costs about 19 us of hipBLASLt host time
+#     against a few for the hand-written GEMM: the eager forward runs 20-26 %
+#     faster on it (1.85 -> 1.37 ms at B*L <= 2048);
+#   * eager, hidden 1536 (K = 1536, the xlarge encoder at 512-2048 rows): the
+#     hand-written GEMM's device time outweighs that saving (3.47 -> 3.82 ms).
+# So below the threshold the projections use the hand-written GEMM only in eager
+# forwards with K <= HIP_GEMM_EAGER_MAX_K, and hipBLASLt otherwise (always while
+# a HIP graph is being captured or torch.compile traces); at 16384 rows the two
+# tie in both modes.  Checked on every call: the layer program binds the fused
+# steps once per bucket, while B varies per call.
 HIP_GEMM_MIN_ROWS = 16384
+HIP_GEMM_EAGER_MAX_K = 768
+
+_GRAPH_CHOICE = False
+
+
+@contextlib.contextmanager
+def graph_gemm_choice():
+    """Eager forwards inside this block pick their GEMMs as HIP-graph capture does
+    (hipBLASLt below :data:`HIP_GEMM_MIN_ROWS` rows), so they reproduce a captured
+    bucket's replays bit for bit."""
+
+    global _GRAPH_CHOICE
+    saved, _GRAPH_CHOICE = _GRAPH_CHOICE, True
+    try:
+        yield
+    finally:
+        _GRAPH_CHOICE = saved
 
 
 def hip_gemm_rows(x: torch.Tensor) -> bool:
-    """True if ``x`` (``[..., K]``) has enough rows for the hand-written GEMM."""
+    """True if the projection of ``x`` (``[..., K]``) runs on the hand-written GEMM."""
 
     k = x.shape[-1]
-    return k > 0 and x.numel() // k >= HIP_GEMM_MIN_ROWS
+    if k <= 0 or x.device.type != "cuda":
+        return False
+    if x.numel() // k >= HIP_GEMM_MIN_ROWS:
+        return True
+    if k > HIP_GEMM_EAGER_MAX_K or _GRAPH_CHOICE or torch.compiler.is_compiling():
+        return False
+    return not torch.cuda.is_current_stream_capturing()
 
 # Tile configuration the encoder asks dflash_linear_fwd for (bits 8.. of its
 # epilogue argument; 0 = the library's choice by shape).  A switch for A/B timing.
@@ -190,8 +224,8 @@ def fusable_intermediate(module: nn.Module) -> bool:
 
 
 def intermediate_block(module: nn.Module, hidden_states: torch.Tensor) -> torch.Tensor:
-    """``module(hidden_states)`` as one GEMM with the GELU in its epilogue (at
-    :data:`HIP_GEMM_MIN_ROWS` rows or more; below, the module itself)."""
+    """``module(hidden_states)`` as one GEMM with the GELU in its epilogue, or the
+    module itself where :func:`hip_gemm_rows` says so."""
 
     if not hip_gemm_rows(hidden_states):
         return module(hidden_states)
@@ -202,8 +236,8 @@ def intermediate_block(module: nn.Module, hidden_states: torch.Tensor) -> torch.
 def output_block_gemm(module: nn.Module, hidden_states: torch.Tensor,
                       input_tensor: torch.Tensor) -> torch.Tensor:
     """``module(hidden_states, input_tensor)``: GEMM with the residual added in its
-    epilogue, then LayerNorm over the sum (one read of it instead of two).  Below
-    :data:`HIP_GEMM_MIN_ROWS` rows: hipBLASLt and the fused add + LayerNorm."""
+    epilogue, then LayerNorm over the sum (one read of it instead of two); where
+    :func:`hip_gemm_rows` says so, hipBLASLt and the fused add + LayerNorm."""
 
     if not hip_gemm_rows(hidden_states):
         return output_block(module, hidden_states, input_tensor)

@@ -363,10 +363,11 @@ def test_hip_graph_buckets_replay_eager_results():
 
     Several replays per bucket with new inputs, interleaved with eager work and
     host synchronisation, each checked against the eager forward of the same
-    inputs (same kernels, same launch order: identical results expected).
+    inputs with the GEMM choice of graph capture (same kernels, same launch order:
+    identical results expected).
     """
 
-    from disentangled_flash import capture_deberta_buckets, enable_deberta_inference
+    from disentangled_flash import capture_deberta_buckets, enable_deberta_inference, layers
 
     base = _encoder_model(2, 768, 12, 3072)
     model = enable_deberta_inference(base.to("cuda", torch.float16), backend="hip",
@@ -382,8 +383,9 @@ def test_hip_graph_buckets_replay_eager_results():
                 hidden, mask = _encoder_inputs(batch, length, 768, seed=100 + replay + length)
                 hidden, mask = hidden.to("cuda", torch.float16), mask.cuda()
                 plans = encoder.plans_for(length)
-                eager = encoder.forward_prepared(hidden, mask, plans,
-                                                 output_hidden_states=False).last_hidden_state
+                with layers.graph_gemm_choice():  # the GEMMs a capture picks
+                    eager = encoder.forward_prepared(hidden, mask, plans,
+                                                     output_hidden_states=False).last_hidden_state
                 torch.cuda.synchronize()
                 got = bucket(hidden, mask).clone()
                 torch.cuda.synchronize()
