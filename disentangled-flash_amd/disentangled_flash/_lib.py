@@ -12,6 +12,7 @@ HIP-backend call raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from pathlib import Path
 
@@ -145,8 +146,43 @@ def check(code: int, what: str) -> None:
         raise RuntimeError(f"{what} failed with code {code}: {message}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def current_stream_handle(device: torch.device) -> int:
+    """The HIP stream torch launches on for ``device`` (raw handle)."""
+
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 
-__all__ = ["DTYPE_CODES", "check", "current_stream_handle", "is_available", "library_path", "load"]
+def hip_op(name: str):
+    """``torch.library.custom_op(name)`` whose eager calls skip the dispatcher.
+
+    Under ``torch.compile`` tracing the function is the custom op (with the fake
+    implementation registered on it), so compiled graphs keep the HIP op as one
+    node.  Called eagerly - and during HIP-graph capture - it runs the
+    implementation directly: the op dispatch adds about 3 us of host time per
+    call, which an eager encoder forward of a few thousand tokens (bound by launch
+    time) pays on every layer.
+    """
+
+    def wrap(impl):
+        op = torch.library.custom_op(name, mutates_args=())(impl)
+
+        @functools.wraps(impl)
+        def call(*args, **kwargs):
+            if torch.compiler.is_compiling():
+                return op(*args, **kwargs)
+            return impl(*args, **kwargs)
+
+        call.register_fake = op.register_fake
+        call.custom_op = op
+        return call
+
+    return wrap
+
+
+__all__ = ["DTYPE_CODES", "check", "current_stream_handle", "hip_op", "is_available",
+           "library_path", "load"]

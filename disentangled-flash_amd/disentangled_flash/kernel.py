@@ -38,7 +38,7 @@ SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 RELATIVE_MODES = ("fused", "table")
 
 
-@torch.library.custom_op("disentangled_flash::deberta_attention", mutates_args=())
+@_lib.hip_op("disentangled_flash::deberta_attention")
 def deberta_attention(
     query: torch.Tensor,
     key: torch.Tensor,
@@ -102,7 +102,7 @@ def _deberta_attention_fake(query, key, value, c2p, p2c, delta_to_local, attenti
     return query.new_empty((batch, sequence_length, num_heads * head_dim))
 
 
-@torch.library.custom_op("disentangled_flash::deberta_attention_rel", mutates_args=())
+@_lib.hip_op("disentangled_flash::deberta_attention_rel")
 def deberta_attention_rel(
     qkv: torch.Tensor,
     pos_key: torch.Tensor,

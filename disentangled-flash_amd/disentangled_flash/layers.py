@@ -29,7 +29,7 @@ from torch.nn import functional as F
 from . import _lib
 
 
-@torch.library.custom_op("disentangled_flash::add_layernorm", mutates_args=())
+@_lib.hip_op("disentangled_flash::add_layernorm")
 def add_layernorm(
     x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float
 ) -> torch.Tensor:
@@ -60,7 +60,7 @@ def _add_layernorm_fake(x, residual, weight, bias, eps):
     return torch.empty_like(x)
 
 
-@torch.library.custom_op("disentangled_flash::layernorm", mutates_args=())
+@_lib.hip_op("disentangled_flash::layernorm")
 def layernorm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float) -> torch.Tensor:
     """``LayerNorm(x)`` over the last dimension (statistics in fp32)."""
 
@@ -144,7 +144,7 @@ GEMM_BIAS_ADD = 2
 GEMM_DTYPES = (torch.float16, torch.bfloat16)
 
 
-@torch.library.custom_op("disentangled_flash::linear_epilogue", mutates_args=())
+@_lib.hip_op("disentangled_flash::linear_epilogue")
 def linear_epilogue(
     x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, residual: torch.Tensor | None,
     epilogue: int
@@ -291,7 +291,7 @@ def output_block(module: nn.Module, hidden_states: torch.Tensor,
 CONV_ACTIVATIONS = {"gelu": 0, "tanh": 1, "relu": 2}
 
 
-@torch.library.custom_op("disentangled_flash::conv_layer_tail", mutates_args=())
+@_lib.hip_op("disentangled_flash::conv_layer_tail")
 def conv_layer_tail(
     taps: torch.Tensor, residual: torch.Tensor, conv_bias: torch.Tensor, weight: torch.Tensor,
     bias: torch.Tensor, mask: torch.Tensor, eps: float, act: int
