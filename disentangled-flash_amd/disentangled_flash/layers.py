@@ -21,6 +21,7 @@ traces through them, like the attention ops.
 from __future__ import annotations
 
 import contextlib
+import threading
 
 import torch
 from torch import nn
@@ -104,21 +105,21 @@ USE_HIP_GEMM = True
 HIP_GEMM_MIN_ROWS = 16384
 HIP_GEMM_EAGER_MAX_K = 768
 
-_GRAPH_CHOICE = False
+_GRAPH_CHOICE = threading.local()
 
 
 @contextlib.contextmanager
 def graph_gemm_choice():
-    """Eager forwards inside this block pick their GEMMs as HIP-graph capture does
-    (hipBLASLt below :data:`HIP_GEMM_MIN_ROWS` rows), so they reproduce a captured
-    bucket's replays bit for bit."""
+    """Eager forwards inside this block (on this thread) pick their GEMMs as HIP-graph
+    capture does (hipBLASLt below :data:`HIP_GEMM_MIN_ROWS` rows), so they reproduce a
+    captured bucket's replays bit for bit."""
 
-    global _GRAPH_CHOICE
-    saved, _GRAPH_CHOICE = _GRAPH_CHOICE, True
+    saved = getattr(_GRAPH_CHOICE, "on", False)
+    _GRAPH_CHOICE.on = True
     try:
         yield
     finally:
-        _GRAPH_CHOICE = saved
+        _GRAPH_CHOICE.on = saved
 
 
 def hip_gemm_rows(x: torch.Tensor) -> bool:
@@ -129,7 +130,8 @@ def hip_gemm_rows(x: torch.Tensor) -> bool:
         return False
     if x.numel() // k >= HIP_GEMM_MIN_ROWS:
         return True
-    if k > HIP_GEMM_EAGER_MAX_K or _GRAPH_CHOICE or torch.compiler.is_compiling():
+    if k > HIP_GEMM_EAGER_MAX_K or getattr(_GRAPH_CHOICE, "on", False) \
+            or torch.compiler.is_compiling():
         return False
     return not torch.cuda.is_current_stream_capturing()
 
