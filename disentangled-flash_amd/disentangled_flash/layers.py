@@ -130,8 +130,9 @@ def hip_gemm_rows(x: torch.Tensor) -> bool:
         return False
     if x.numel() // k >= HIP_GEMM_MIN_ROWS:
         return True
-    if k > HIP_GEMM_EAGER_MAX_K or getattr(_GRAPH_CHOICE, "on", False) \
-            or torch.compiler.is_compiling():
+    if torch.compiler.is_compiling():
+        return False
+    if k > HIP_GEMM_EAGER_MAX_K or getattr(_GRAPH_CHOICE, "on", False):
         return False
     return not torch.cuda.is_current_stream_capturing()
 
