@@ -256,6 +256,14 @@ DFLASH_API int dflash_conv_layer_tail_fwd(const void* z, int z_dtype, const void
  * N must be a multiple of 128 or 192 and K of 32 (DFLASH_ERR_SHAPE otherwise;
  * every projection of DeBERTa base/large/xlarge qualifies); x, weight, residual, y
  * 16-byte aligned, bias 8-byte aligned.  M == 0 is a no-op.
+ *   epilogue : the code above in bits 0-7; bits 8 and up select a tile
+ *              configuration (0 = automatic by N and epilogue): 1 = 256 x 192
+ *              tiles, 4 wavefronts; 2 = 256 x 128 at two workgroups per CU
+ *              (N % 128 == 0); 3 = 256 x 192, 8 wavefronts (N % 192 == 0);
+ *              4 = 64 x 128 at three per CU (N % 128 == 0); 5 = 64 x 64 at four
+ *              per CU (N % 64 == 0).  The 64-row forms give four times the tiles
+ *              for few rows.  A configuration that does not fit N returns
+ *              DFLASH_ERR_SHAPE.
  */
 DFLASH_API int dflash_linear_fwd(const void* x, const void* weight, const void* bias,
                                  const void* residual, void* y, int M, int N, int K,
