@@ -258,7 +258,7 @@ DFLASH_API int dflash_conv_layer_tail_fwd(const void* z, int z_dtype, const void
  * 16-byte aligned, bias 8-byte aligned.  M == 0 is a no-op.
  *   epilogue : the code above in bits 0-7; bits 8 and up select a tile
  *              configuration (0 = automatic by N and epilogue): 1 = 256 x 192
- *              tiles, 4 wavefronts; 2 = 256 x 128 at two workgroups per CU
+ *              tiles, 4 wavefronts (N % 192 == 0); 2 = 256 x 128 at two workgroups per CU
  *              (N % 128 == 0); 3 = 256 x 192, 8 wavefronts (N % 192 == 0);
  *              4 = 64 x 128 at three per CU (N % 128 == 0); 5 = 64 x 64 at four
  *              per CU (N % 64 == 0).  The 64-row forms give four times the tiles
