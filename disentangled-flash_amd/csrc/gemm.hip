@@ -410,8 +410,25 @@ int launch_gemm(GemmArgs args, hipStream_t stream) {
   return static_cast<int>(hipGetLastError());
 }
 
+// CUs of the current device (cached per device; 256 if it cannot be read).
+int gemm_device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int known = cache[dev].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  if (dev < 64) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
 // config: 0 = automatic, 1 = CfgWide, 2 = CfgPair, 3 = CfgEight, 4 = CfgSmall,
-// 5 = CfgTiny.  Automatic
+// 5 = CfgTiny.  Automatic, for grids that fill at least half the CUs
 // (measured at M = 16384, fp16): CfgEight where N % 192 == 0 (QKV 71.7 us,
 // hidden-wide dense 24.5 us), except the GELU epilogue, whose VALU work
 // overlaps better at two workgroups per CU (CfgPair, FFN intermediate 108.5
@@ -420,7 +437,16 @@ template <typename T, int EPI>
 int pick_config(const GemmArgs& args, int config, hipStream_t stream) {
   const bool wide_ok = args.N % CfgWide::BN == 0;
   const bool pair_ok = args.N % CfgPair::BN == 0;
-  if (config == 0) config = (wide_ok && !(EPI == kEpiBiasGelu && pair_ok)) ? 3 : 2;
+  if (config == 0) {
+    config = (wide_ok && !(EPI == kEpiBiasGelu && pair_ok)) ? 3 : 2;
+    // Few rows: when the 256-row grid would give fewer tiles than half the CUs,
+    // the 64-row forms (four times the tiles) are faster on the device, 64 x 64
+    // up to 1024 rows and 64 x 128 above (HIP-graph timings at 512 and 2048 rows:
+    // e.g. a 2304-wide projection of 512 x 768 in 7.0 against 17.6 us).
+    const int bn = config == 3 ? CfgEight::BN : CfgPair::BN;
+    const int64_t tiles = static_cast<int64_t>((args.M + 255) / 256) * (args.N / bn);
+    if (2 * tiles < gemm_device_cus()) config = (args.M <= 1024 || !pair_ok) ? 5 : 4;
+  }
   switch (config) {
     case 1:
       return wide_ok ? launch_gemm<T, EPI, CfgWide>(args, stream) : DFLASH_ERR_SHAPE;

@@ -350,7 +350,7 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
                 "fused QKV projection is not prepared; call prepare_for_inference() first"
             )
         if layers.USE_HIP_GEMM and hidden_states.device.type == "cuda" \
-                and layers.hip_gemm_rows(hidden_states) \
+                and layers.hip_gemm_rows(hidden_states, prep.qkv_weight.shape[0]) \
                 and gemm_fits(prep.qkv_weight, prep.qkv_bias) \
                 and hidden_states.dtype == prep.qkv_weight.dtype:
             return linear_epilogue(gemm_rows(hidden_states), prep.qkv_weight, prep.qkv_bias, None,

@@ -86,24 +86,28 @@ def _layernorm_fake(x, weight, bias, eps):
 # an encoder is prepared and on every QKV projection.  A switch for A/B timing.
 USE_HIP_GEMM = True
 
-# Fewest rows (tokens, M = B*L) for which the encoder projections always run on
-# the hand-written GEMM.  Measured on whole encoders (12-layer base fp16, 24-layer
-# xlarge bf16), below it the choice depends on how the forward is launched:
-#   * HIP-graph replay: hipBLASLt plus a separate GELU is faster on the device (up
-#     to 1.5x at 512 rows: the GEMM's 256-row tiles leave most CUs idle);
-#   * eager, hidden 768 (K = 768): a forward at a few thousand rows is bound by
-#     launch time, and an F.linear call costs about 19 us of hipBLASLt host time
-#     against a few for the hand-written GEMM: the eager forward runs 20-26 %
-#     faster on it (1.85 -> 1.37 ms at B*L <= 2048);
-#   * eager, hidden 1536 (K = 1536, the xlarge encoder at 512-2048 rows): the
-#     hand-written GEMM's device time outweighs that saving (3.47 -> 3.82 ms).
-# So below the threshold the projections use the hand-written GEMM only in eager
-# forwards with K <= HIP_GEMM_EAGER_MAX_K, and hipBLASLt otherwise (always while
-# a HIP graph is being captured or torch.compile traces); at 16384 rows the two
-# tie in both modes.  Checked on every call: the layer program binds the fused
-# steps once per bucket, while B varies per call.
+# Which GEMM runs an encoder projection, by rows (tokens, M = B*L), width and
+# launch mode.  Measured on whole encoders (12-layer base fp16, 24-layer xlarge
+# bf16) and per GEMM in HIP graphs:
+#   * HIP-graph replay: below HIP_GEMM_MIN_ROWS rows hipBLASLt (plus a separate
+#     GELU) is faster on the device, up to 1.5x at 512 rows; at 16384 rows the
+#     two tie;
+#   * eager, up to HIP_GEMM_EAGER_MAX_ROWS rows: the forward is bound by launch
+#     time, and an F.linear call costs about 19 us of hipBLASLt host time against
+#     a few for the hand-written GEMM.  For base-width projections (N or K at
+#     most HIP_GEMM_EAGER_MAX_WIDTH) that wins (1.85 -> 1.0-1.2 ms per forward);
+#     for the xlarge widths (N, K >= 1536) the hand-written kernel's device time
+#     outweighs it (3.47 -> 3.82 ms), and from about 4096 rows eager forwards are
+#     device-bound again.
+# So: the hand-written GEMM from HIP_GEMM_MIN_ROWS rows (QKV, attention-output
+# dense, FFN intermediate; the FFN output dense, K = 4 x hidden, stays on
+# hipBLASLt there), and in eager forwards up to HIP_GEMM_EAGER_MAX_ROWS rows at
+# base width; hipBLASLt otherwise, and always while a HIP graph is being captured
+# or torch.compile traces.  Checked on every call: the layer program binds the
+# fused steps once per bucket, while B varies per call.
 HIP_GEMM_MIN_ROWS = 16384
-HIP_GEMM_EAGER_MAX_K = 768
+HIP_GEMM_EAGER_MAX_ROWS = 2048
+HIP_GEMM_EAGER_MAX_WIDTH = 768
 
 _GRAPH_CHOICE = threading.local()
 
@@ -122,19 +126,31 @@ def graph_gemm_choice():
         _GRAPH_CHOICE.on = saved
 
 
-def hip_gemm_rows(x: torch.Tensor) -> bool:
-    """True if the projection of ``x`` (``[..., K]``) runs on the hand-written GEMM."""
+def eager_small_gemm(x: torch.Tensor, n: int) -> bool:
+    """True for an eager ``[..., K] x [N, K]^T`` projection small enough to be
+    launch-bound, at base width (see the rules above)."""
+
+    k = x.shape[-1]
+    if k <= 0 or x.device.type != "cuda" or torch.compiler.is_compiling():
+        return False
+    if x.numel() // k > HIP_GEMM_EAGER_MAX_ROWS or min(k, n) > HIP_GEMM_EAGER_MAX_WIDTH:
+        return False
+    if getattr(_GRAPH_CHOICE, "on", False):
+        return False
+    return not torch.cuda.is_current_stream_capturing()
+
+
+def hip_gemm_rows(x: torch.Tensor, n: int | None = None) -> bool:
+    """True if the projection of ``x`` (``[..., K]``) to ``n`` columns (default K)
+    runs on the hand-written GEMM."""
 
     k = x.shape[-1]
     if k <= 0 or x.device.type != "cuda":
         return False
     if x.numel() // k >= HIP_GEMM_MIN_ROWS:
         return True
-    if torch.compiler.is_compiling():
-        return False
-    if k > HIP_GEMM_EAGER_MAX_K or getattr(_GRAPH_CHOICE, "on", False):
-        return False
-    return not torch.cuda.is_current_stream_capturing()
+    return eager_small_gemm(x, k if n is None else n)
+
 
 # Tile configuration the encoder asks dflash_linear_fwd for (bits 8.. of its
 # epilogue argument; 0 = the library's choice by shape).  A switch for A/B timing.
@@ -230,7 +246,7 @@ def intermediate_block(module: nn.Module, hidden_states: torch.Tensor) -> torch.
     """``module(hidden_states)`` as one GEMM with the GELU in its epilogue, or the
     module itself where :func:`hip_gemm_rows` says so."""
 
-    if not hip_gemm_rows(hidden_states):
+    if not hip_gemm_rows(hidden_states, module.dense.out_features):
         return module(hidden_states)
     return linear_epilogue(gemm_rows(hidden_states), module.dense.weight, module.dense.bias,
                            None, GEMM_BIAS_GELU)
@@ -242,7 +258,7 @@ def output_block_gemm(module: nn.Module, hidden_states: torch.Tensor,
     epilogue, then LayerNorm over the sum (one read of it instead of two); where
     :func:`hip_gemm_rows` says so, hipBLASLt and the fused add + LayerNorm."""
 
-    if not hip_gemm_rows(hidden_states):
+    if not hip_gemm_rows(hidden_states, module.dense.out_features):
         return output_block(module, hidden_states, input_tensor)
     summed = linear_epilogue(gemm_rows(hidden_states), module.dense.weight, module.dense.bias,
                              gemm_rows(input_tensor), GEMM_BIAS_ADD)
@@ -279,13 +295,21 @@ def output_block(module: nn.Module, hidden_states: torch.Tensor,
                  input_tensor: torch.Tensor) -> torch.Tensor:
     """``module(hidden_states, input_tensor)`` with the residual add and LayerNorm fused.
 
-    The caller checks :func:`fusable_output_block` once when the encoder is
-    prepared; this function is the hot path.
+    The dense runs on hipBLASLt, or in launch-bound eager forwards at base width
+    (:func:`eager_small_gemm`) on the hand-written GEMM with the residual in its
+    epilogue.  The caller checks :func:`fusable_output_block` once when the
+    encoder is prepared; this function is the hot path.
     """
 
-    projected = F.linear(hidden_states, module.dense.weight, module.dense.bias)
+    dense = module.dense
     residual = input_tensor if input_tensor.is_contiguous() else input_tensor.contiguous()
     norm = module.LayerNorm
+    if USE_HIP_GEMM and eager_small_gemm(hidden_states, dense.out_features) \
+            and gemm_fits(dense.weight, dense.bias) and hidden_states.dtype == dense.weight.dtype:
+        summed = linear_epilogue(gemm_rows(hidden_states), dense.weight, dense.bias, residual,
+                                 GEMM_BIAS_ADD)
+        return layernorm(summed, norm.weight, norm.bias, norm.eps)
+    projected = F.linear(hidden_states, dense.weight, dense.bias)
     return add_layernorm(projected, residual, norm.weight, norm.bias, norm.eps)
 
 
