@@ -95,7 +95,8 @@ USE_HIP_GEMM = True
 #   * eager, up to HIP_GEMM_EAGER_MAX_ROWS rows: the forward is bound by launch
 #     time, and an F.linear call costs about 19 us of hipBLASLt host time against
 #     a few for the hand-written GEMM.  For base-width projections (N or K at
-#     most HIP_GEMM_EAGER_MAX_WIDTH) that wins (1.85 -> 1.0-1.2 ms per forward);
+#     most HIP_GEMM_EAGER_MAX_WIDTH) that wins (1.85 -> 1.37 ms per forward at
+#     B*L <= 2048; 0.8-1.0 ms with the library's 64-row tiles at these rows);
 #     for the xlarge widths (N, K >= 1536) the hand-written kernel's device time
 #     outweighs it (3.47 -> 3.82 ms), and from about 4096 rows eager forwards are
 #     device-bound again.
