@@ -737,6 +737,11 @@ def main() -> int:
             "hip_fast_max_abs_err_vs_original": _sig(fast32["hip_max_abs_err_vs_original"]),
         }
         log(f"encoder fp32: {line['encoder']['fp32']}")
+        # A launch-bound C3 cell (B=8, L=128): eager forward_prepared, as the reference's
+        # benchmark times it (benchmark_cuda.py:781-782), and the HIP-graph replay.
+        small = bench_sweep(args.encoder_steps, 3, batches=(8,), lengths=(128,))[0]
+        line["encoder"]["c3_b8_l128"] = {k: _sig(v) for k, v in small.items()
+                                         if k not in ("batch", "seq_len")}
     if not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline()
         log(f"cpu baseline: {line['cpu_baseline']}")
