@@ -154,3 +154,33 @@ def test_encoder_gemm_tails_match_modules(monkeypatch):
     print(f"intermediate {err_i:.3e}, self-output {err_o:.3e}")
     assert err_i <= 4e-3
     assert err_o <= 2e-2  # LayerNorm output of O(1) rows in fp16 (rstd ~ 1, two roundings)
+
+
+def test_projection_dispatch_rules():
+    """Which GEMM an encoder projection runs on, by rows, width and launch mode: the
+    hand-written GEMM from HIP_GEMM_MIN_ROWS rows and in launch-bound eager forwards at
+    base width; hipBLASLt otherwise, in particular while a HIP graph is captured."""
+
+    from disentangled_flash import layers
+
+    base = torch.zeros(1, 512, 768, device="cuda", dtype=torch.float16)      # 512 rows, K 768
+    xlarge = torch.zeros(1, 512, 1536, device="cuda", dtype=torch.float16)   # K 1536
+    big = torch.zeros(32, 512, 768, device="cuda", dtype=torch.float16)      # 16384 rows
+    mid = torch.zeros(8, 512, 768, device="cuda", dtype=torch.float16)       # 4096 rows
+    assert layers.hip_gemm_rows(base) and layers.hip_gemm_rows(base, 2304)
+    assert layers.eager_small_gemm(torch.zeros(1, 512, 3072, device="cuda", dtype=torch.float16), 768)
+    assert not layers.hip_gemm_rows(xlarge) and not layers.hip_gemm_rows(xlarge, 4608)
+    assert layers.hip_gemm_rows(big) and not layers.eager_small_gemm(big, 768)
+    assert not layers.hip_gemm_rows(mid)
+    assert not layers.hip_gemm_rows(base.cpu())
+    with layers.graph_gemm_choice():
+        assert not layers.hip_gemm_rows(base) and layers.hip_gemm_rows(big)
+    assert layers.hip_gemm_rows(base)
+    graph = torch.cuda.CUDAGraph()
+    seen = []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side), torch.cuda.graph(graph, stream=side):
+        seen.append((layers.hip_gemm_rows(base), layers.hip_gemm_rows(big)))
+    torch.cuda.current_stream().wait_stream(side)
+    assert seen == [(False, True)]
