@@ -369,6 +369,77 @@ def bench_sweep(steps: int, warmup: int, batches=(1, 8, 16, 32),
     return rows
 
 
+def bench_gemm_table(reps: int = 20):
+    """Per-GEMM device time of the encoder projections, hipBLASLt against the
+    hand-written GEMM's tile configurations, at C3 (base, fp16) and C4 (xlarge,
+    bf16) widths and few to many rows.  Each entry replays a HIP graph of ``reps``
+    back-to-back calls, so host launch cost is excluded; us per call.  hipBLASLt
+    is ``F.linear`` (plus ``F.gelu`` for the intermediate; the residual of the
+    dense layers folds into the following add + LayerNorm there)."""
+
+    import torch.nn.functional as F
+
+    from disentangled_flash import _lib
+
+    lib = _lib.load()
+
+    def graph_us(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                fn()
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(10):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / 10 / reps * 1e3
+
+    gen = torch.Generator().manual_seed(31)
+    rows = []
+    for width, dtype, row_counts in ((768, torch.float16, (512, 2048, 8192, 16384)),
+                                     (1536, torch.bfloat16, (512, 2048))):
+        shapes = (("qkv", width, 3 * width, 0), ("attention_output", width, width, 2),
+                  ("ffn_intermediate_gelu", width, 4 * width, 1),
+                  ("ffn_output", 4 * width, width, 2))
+        for m in row_counts:
+            for name, k, n, epilogue in shapes:
+                x = (torch.randn(m, k, generator=gen) * 0.5).to("cuda", dtype)
+                w = (torch.randn(n, k, generator=gen) * 0.02).to("cuda", dtype)
+                b = (torch.randn(n, generator=gen) * 0.02).to("cuda", dtype)
+                r = torch.randn(m, n, generator=gen).to("cuda", dtype)
+                y = torch.empty(m, n, device="cuda", dtype=dtype)
+                if epilogue == 1:
+                    library = graph_us(lambda: F.gelu(F.linear(x, w, b)))  # noqa: B023
+                else:
+                    library = graph_us(lambda: F.linear(x, w, b))  # noqa: B023
+                row = {"hidden": width, "dtype": str(dtype).replace("torch.", ""), "rows": m,
+                       "gemm": name, "hipblaslt_us": round(library, 2)}
+                for config in (2, 3, 4, 5):
+                    def call(config=config):
+                        return lib.dflash_linear_fwd(
+                            x.data_ptr(), w.data_ptr(), b.data_ptr(), r.data_ptr(),  # noqa: B023
+                            y.data_ptr(), m, n, k, epilogue | (config << 8),  # noqa: B023
+                            _lib.DTYPE_CODES[dtype], _lib.current_stream_handle(x.device))  # noqa: B023
+                    if call() != 0:
+                        continue
+                    row[f"config{config}_us"] = round(graph_us(call), 2)
+                log(json.dumps(row))
+                rows.append(row)
+    return rows
+
+
 def bench_edge(steps: int, warmup: int):
     """C5 edge sweep: the fused attention op for d=128/H=8 (B=16, L=512) and d=32/H=16
     (B=16, L=384) in fp16/bf16/fp32 x {c2p, p2c, c2p|p2c}, boundary valid lengths
@@ -592,6 +663,9 @@ def main() -> int:
                         help="C5 head-dim / precision / mode sweep of the fused op, one JSON line")
     parser.add_argument("--c4", action="store_true",
                         help="C4 24-layer xlarge bf16 encoder per bucket, one JSON line")
+    parser.add_argument("--gemm-table", action="store_true",
+                        help="per-GEMM device times in HIP graphs, hipBLASLt vs the hand-written "
+                             "configurations, one JSON line")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="one 256 MiB device-to-device copy (HBM counter calibration)")
     args = parser.parse_args()
@@ -635,6 +709,10 @@ def main() -> int:
     if args.encoder_only:
         enc = bench_encoder(32, 512, args.encoder_steps, 3, backends=("hip",))
         log(f"encoder: {enc}")
+        return 0
+    if args.gemm_table:
+        print(json.dumps({"gemm_table": "us per call, HIP-graph replay", "rows": bench_gemm_table()}),
+              flush=True)
         return 0
     if args.tile_sweep:
         print(json.dumps({"tile_sweep": "fused fp16 c2p|p2c, unsplit, us",
