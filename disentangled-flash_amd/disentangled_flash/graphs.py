@@ -23,6 +23,7 @@ from collections.abc import Iterable
 
 import torch
 
+from . import layers
 from .deberta import DebertaV2InferenceEncoder
 
 
@@ -57,8 +58,11 @@ class DebertaGraphBucket:
         side = torch.cuda.Stream(device=weight.device)
         side.wait_stream(torch.cuda.current_stream(weight.device))
         with torch.inference_mode(), torch.cuda.stream(side):
-            for _ in range(max(1, warmup)):  # library handles and workspaces exist before capture
-                run()
+            # Library handles and workspaces exist before capture: the warm-up runs the
+            # kernels the capture will record (capture picks hipBLASLt for few rows).
+            with layers.graph_gemm_choice():
+                for _ in range(max(1, warmup)):
+                    run()
             with torch.cuda.graph(self.graph, pool=self.pool, stream=side):
                 self.output = run()
         torch.cuda.current_stream(weight.device).wait_stream(side)
