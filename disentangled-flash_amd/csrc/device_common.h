@@ -54,83 +54,9 @@ struct Mma<float> {
   }
 };
 
-// Load one lane's k-slice starting at `base` (which already points at k0 of
-// the MFMA step for this lane's row/column).
-template <typename T>
-__device__ inline typename Mma<T>::frag load_slice(const T* base, int g) {
-  if constexpr (Mma<T>::PER == 8) {
-    return *reinterpret_cast<const typename Mma<T>::frag*>(base + 8 * g);
-  } else {
-    return base[g];
-  }
-}
-
-template <typename T>
-__device__ inline typename Mma<T>::frag zero_frag() {
-  typename Mma<T>::frag z;
-  if constexpr (Mma<T>::PER == 8) {
-    for (int e = 0; e < 8; ++e) z[e] = static_cast<T>(0.0f);
-  } else {
-    z = 0.0f;
-  }
-  return z;
-}
-
-template <typename T>
-__device__ inline T to_t(float x) {
-  return static_cast<T>(x);
-}
-
-template <typename T>
-__device__ inline float to_f(T x) {
-  return static_cast<float>(x);
-}
-
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-
-struct Params {
-  const void* q;
-  const void* k;
-  const void* v;
-  int64_t sb, sh, sl;          // element strides of q/k/v: batch, head, position
-  const void* pos_key;         // c2p table [B, H, L, S]
-  const void* pos_query;       // p2c table [B, H, L, S]
-  const int32_t* lut;          // delta_to_local [2L-1]
-  const uint8_t* mask;         // [B, L], nonzero = kept
-  void* out;                   // [B, L, H*D]
-  int B, H, L, S;
-  int nqb;                     // query blocks per (b, h)
-  float scale_log2;            // log2(e) / sqrt(d * factor)
-};
-
-// Padded LDS row lengths (elements).  16-bit rows stay 16-byte aligned.
-template <typename T>
-constexpr int pad_of() {
-  return sizeof(T) == 2 ? 8 : 4;
-}
-
-template <typename T, int D, int BN, int QW>
-struct Layout {
-  static constexpr int kQueriesPerWave = QW;                     // query rows per wavefront
-  static constexpr int kBlockM = kWaves * QW;                    // query rows per workgroup
-  static constexpr int kPad = pad_of<T>();
-  static constexpr int KS_LD = D + kPad;                         // Ks[BN][KS_LD]
-  static constexpr int VT_LD = BN + 4;                           // Vt[D][VT_LD]
-  static constexpr int LW_N = kBlockM + BN;                      // lut window
-
-  static constexpr size_t ks_bytes = size_t(BN) * KS_LD * sizeof(T);
-  static constexpr size_t vt_bytes = size_t(D) * VT_LD * sizeof(T);
-  static constexpr size_t lw_bytes = size_t(LW_N) * sizeof(int32_t);
-  static constexpr size_t kb_bytes = size_t(BN) * sizeof(float);
-
-  static constexpr size_t ks_off = 0;
-  static constexpr size_t vt_off = ks_off + ks_bytes;
-  static constexpr size_t kb_off = vt_off + vt_bytes;
-  static constexpr size_t lw_off = kb_off + kb_bytes;
-  static constexpr size_t bytes = lw_off + lw_bytes;
-};
 
 // Workgroup barrier that orders LDS traffic only.  __syncthreads() also waits
 // for every outstanding global load (vmcnt(0)), which would force the
@@ -139,8 +65,6 @@ struct Layout {
 __device__ inline void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-
-__device__ inline int clampi(int x, int lo, int hi) { return x < lo ? lo : (x > hi ? hi : x); }
 
 // Physical workgroup n runs on XCD n % 8.  Renumber so that the query blocks
 // of one (b, h) - which share K, V and the relative tables - land on the same

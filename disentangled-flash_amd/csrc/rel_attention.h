@@ -33,6 +33,10 @@ struct RelParams {
   // fp32 only: 1 = products on the bf16 matrix unit in three parts
   // (fp32_precision="fast"), 0 = IEEE fp32 MFMA.
   int fast;
+  // 1 = pos_key / pos_query are the precomputed c2p / p2c tables [B, H, L, S]
+  // (the reference op's contract) instead of the relative rows [H, S, D].
+  // Unsplit, QW = 32 (d <= 64) or 16 (d = 128), IEEE fp32.
+  int table;
 };
 
 // fp16 / bf16 / fp32, D in {32, 64, 128}; arguments already validated by the

@@ -49,6 +49,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <numeric>
 #include <type_traits>
 
 #include <cstdlib>
@@ -258,9 +259,14 @@ struct RelLayout {
 }  // namespace
 
 template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C, bool SPLIT,
-          bool FAST = false>
+          bool FAST = false, bool TABLE = false>
 __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
   static_assert(!FAST || sizeof(T) == 4, "the bf16x3 form is for fp32 data");
+  static_assert(!(TABLE && (FAST || SPLIT)), "the table form runs unsplit and in IEEE fp32");
+  // Relative windows built on the matrix unit from Kr / Qr rows (MC, MP), or
+  // read from precomputed c2p / p2c tables (TABLE).
+  constexpr bool MC = C2P && !TABLE;
+  constexpr bool MP = P2C && !TABLE;
   using M = std::conditional_t<FAST, RelMmaFast, RelMma<T>>;
   using F = typename M::frag;
   // Fragments that feed several products: split once in the fast fp32 form.
@@ -445,14 +451,128 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     return load_frag<T>(r, static_cast<uint32_t>(slot) * (D * ES) + 32 * kd * ES + sub);
   };
 
-  int lutc[C2P ? kSlide : 1];   // next tile's new c2p chunks
+  int lutc[MC ? kSlide : 1];   // next tile's new c2p chunks
   int lutp = 0;                 // next tile's new p2c chunk (pc = wave)
-  F crow[C2P ? kSlide : 1][KD];  // rows of this tile's new c2p chunks
-  Quad<T> ccar[C2P && kCarry > 0 ? kCarry : 1][kQB];  // c2p values carried into chunks >= kSlide
-  QF prow[P2C ? PU : 1][KD];    // rows of this wavefront's p2c chunks wave + 4u
+  F crow[MC ? kSlide : 1][KD];  // rows of this tile's new c2p chunks
+  Quad<T> ccar[MC && kCarry > 0 ? kCarry : 1][kQB];  // c2p values carried into chunks >= kSlide
+  QF prow[MP ? PU : 1][KD];    // rows of this wavefront's p2c chunks wave + 4u
   // Fast fp32: prow is kept split; the chunk loaded at the end of a tile waits
   // here (unsplit, its load in flight) until the next tile's p2c products.
   F prow_in[FAST && P2C ? KD : 1];
+
+  // ---- table form: the windows read from c2p / p2c tables [B, H, L, S] ----
+  //   Cw[q][t]  = c2p[i0w + q][slot(dlo_w + t)],   Pw[jr][t] = p2c[j0 + jr][slot(dlo + t)],
+  // the values the matrix unit computes in the other form (a table holds the
+  // products Q.Kr / K.Qr rounded to T).  Lanes run along the delta axis, so one
+  // load instruction reads consecutive slots of one or two table rows.  Element
+  // e = lane + 64k of the wavefront's QW x NCW c2p window is (q, t) =
+  // (e / NCW, e % NCW): t repeats with period TC_P in k while q advances by TC_R
+  // per period, so a lane needs TC_P lookups per tile.  The p2c window (BN x NPW)
+  // is split the same way over the workgroup's threads (e = tid + 256k).  Loads
+  // of tile n+1 are issued after the gathers of tile n and stored after barrier
+  // B of tile n+1 (every wavefront is past its gathers of tile n then).
+  constexpr int NCW = NCC * 16;
+  constexpr int NPW = NPC * 16;
+  constexpr bool TC = TABLE && C2P;
+  constexpr bool TP = TABLE && P2C;
+  constexpr int TC_P = TC ? NCW / std::gcd(64, NCW) : 1;
+  constexpr int TC_R = TC ? 64 * TC_P / NCW : 0;
+  constexpr int TC_N = TC ? QW * NCW / 64 : 1;
+  constexpr int TP_P = TP ? NPW / std::gcd(kThreads, NPW) : 1;
+  constexpr int TP_R = TP ? kThreads * TP_P / NPW : 0;
+  constexpr int TP_N = TP ? BN * NPW / kThreads : 1;
+  static_assert(!TC || (QW * NCW % 64 == 0 && TC_N % TC_P == 0), "c2p window in whole loads");
+  static_assert(!TP || (BN * NPW % kThreads == 0 && TP_N % TP_P == 0), "p2c window in whole loads");
+  using TW = std::conditional_t<sizeof(T) == 2, uint16_t, uint32_t>;
+  const uint32_t row_bytes = static_cast<uint32_t>(p.S) * ES;  // one table row
+  const int64_t tab_off = (static_cast<int64_t>(b) * p.H + h) * L * p.S;
+  const auto rtc = make_rsrc(reinterpret_cast<const T*>(p.pos_key) + tab_off,
+                             static_cast<uint32_t>(L) * row_bytes);
+  const auto rtp = make_rsrc(reinterpret_cast<const T*>(p.pos_query) + tab_off,
+                             static_cast<uint32_t>(L) * row_bytes);
+  int tc_q[TC_P], tc_t[TC_P], tc_slot[TC_P];
+  int tp_j[TP_P], tp_t[TP_P], tp_slot[TP_P];
+#pragma unroll
+  for (int pp = 0; pp < TC_P; ++pp) {
+    const int e = lane + 64 * pp;
+    tc_q[pp] = TC ? e / NCW : 0;
+    tc_t[pp] = TC ? e % NCW : 0;
+    tc_slot[pp] = 0;
+  }
+#pragma unroll
+  for (int pp = 0; pp < TP_P; ++pp) {
+    const int e = tid + kThreads * pp;
+    tp_j[pp] = TP ? e / NPW : 0;
+    tp_t[pp] = TP ? e % NPW : 0;
+    tp_slot[pp] = 0;
+  }
+  TW tcv[TC_N];
+  TW tpv[TP_N];
+  auto load_tw = [](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) -> TW {
+    if constexpr (sizeof(T) == 2) {
+      return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    } else {
+      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+  };
+  // Slots of the windows of the tile at key offset j0.
+  auto table_lookups = [&](int j0) {
+    if constexpr (TC) {
+#pragma unroll
+      for (int pp = 0; pp < TC_P; ++pp)
+        tc_slot[pp] = lut_load(i0w - j0 - (BN - 1) + tc_t[pp] + L - 1);
+    }
+    if constexpr (TP) {
+#pragma unroll
+      for (int pp = 0; pp < TP_P; ++pp)
+        tp_slot[pp] = lut_load(i0 - j0 - (BN - 1) + tp_t[pp] + L - 1);
+    }
+  };
+  // Window values of the tile at key offset j0 (slots from table_lookups(j0)).
+  // Rows past L read as zero through the buffer bounds.
+  auto table_load = [&](int j0) {
+    if constexpr (TC) {
+#pragma unroll
+      for (int pp = 0; pp < TC_P; ++pp) {
+        const uint32_t voff = static_cast<uint32_t>(tc_slot[pp]) * ES +
+                              static_cast<uint32_t>(i0w + tc_q[pp]) * row_bytes;
+#pragma unroll
+        for (int m = 0; m < TC_N / TC_P; ++m)
+          tcv[pp + TC_P * m] = load_tw(rtc, voff, static_cast<uint32_t>(m * TC_R) * row_bytes);
+      }
+    }
+    if constexpr (TP) {
+#pragma unroll
+      for (int pp = 0; pp < TP_P; ++pp) {
+        const uint32_t voff = static_cast<uint32_t>(tp_slot[pp]) * ES +
+                              static_cast<uint32_t>(j0 + tp_j[pp]) * row_bytes;
+#pragma unroll
+        for (int m = 0; m < TP_N / TP_P; ++m)
+          tpv[pp + TP_P * m] = load_tw(rtp, voff, static_cast<uint32_t>(m * TP_R) * row_bytes);
+      }
+    }
+  };
+  auto table_store = [&]() {
+    if constexpr (TC) {
+      T* cw_w = Cw + wave * QW * LY::CW_LD;
+#pragma unroll
+      for (int pp = 0; pp < TC_P; ++pp) {
+        T* dst = cw_w + tc_q[pp] * LY::CW_LD + tc_t[pp];
+#pragma unroll
+        for (int m = 0; m < TC_N / TC_P; ++m)
+          dst[m * TC_R * LY::CW_LD] = __builtin_bit_cast(T, tcv[pp + TC_P * m]);
+      }
+    }
+    if constexpr (TP) {
+#pragma unroll
+      for (int pp = 0; pp < TP_P; ++pp) {
+        T* dst = Pw + tp_j[pp] * LY::PW_LD + tp_t[pp];
+#pragma unroll
+        for (int m = 0; m < TP_N / TP_P; ++m)
+          dst[m * TP_R * LY::PW_LD] = __builtin_bit_cast(T, tpv[pp + TP_P * m]);
+      }
+    }
+  };
 
   // ---- prefetch registers (K, V, mask of the next tile) ----
   u32x4_t pk[NCH];
@@ -546,9 +666,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // c2p window of a tile: the kSlide new chunks are multiplied from crow (the
   // products stay in registers until the previous tile's gathers are done),
   // the kCarry old ones come from ccar.
-  Quad<T> cnew[C2P ? kSlide : 1][kQB];
+  Quad<T> cnew[MC ? kSlide : 1][kQB];
   auto c2p_products = [&]() {
-    if constexpr (C2P) {
+    if constexpr (MC) {
       if constexpr (FAST) {
         // Each row fragment split once for its kQB products.
 #pragma unroll
@@ -580,7 +700,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   };
   auto c2p_store = [&]() {
-    if constexpr (C2P) {
+    if constexpr (MC) {
       T* cw_w = Cw + wave * QW * LY::CW_LD;
       // Queries of block qb meet window indices [16qb, 16qb + BN + 14]: chunks
       // outside [qb, qb + KB] are not stored (they are still multiplied when a
@@ -607,7 +727,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // Rows of the new c2p chunks of tile jt (lookups in lutc), then the lookups
   // of tile jt + BN.
   auto load_crow = [&](int jt) {
-    if constexpr (C2P) {
+    if constexpr (MC) {
 #pragma unroll
       for (int ch = 0; ch < kSlide; ++ch)
 #pragma unroll
@@ -619,15 +739,16 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   // ---- prologue: loads of tile 0, in the order their results are needed ----
   // Lookups first (they depend only on the block).
-  int lc[C2P ? NCC : 1];
-  int lp[P2C ? PU : 1];
-  if constexpr (C2P) {
+  table_lookups(jstart);
+  int lc[MC ? NCC : 1];
+  int lp[MP ? PU : 1];
+  if constexpr (MC) {
 #pragma unroll
     for (int ch = 0; ch < NCC; ++ch) lc[ch] = lut_load(lut_c_index(jstart, ch));
 #pragma unroll
     for (int ch = 0; ch < kSlide; ++ch) lutc[ch] = lut_load(lut_c_index(jstart + BN, ch));
   }
-  if constexpr (P2C) {
+  if constexpr (MP) {
 #pragma unroll
     for (int u = 0; u < PU; ++u) lp[u] = lut_load(lut_p_index(jstart, u));
     lutp = lut_load(lut_p_index(jstart + BN, 0));
@@ -676,8 +797,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   // Rows of the tile-0 windows, then Q and the K/V of tile 0 (a workgroup
   // without kept queries has left before issuing them).
-  F r0[C2P && kCarry > 0 ? kCarry : 1][KD];
-  if constexpr (C2P) {
+  table_load(jstart);
+  F r0[MC && kCarry > 0 ? kCarry : 1][KD];
+  if constexpr (MC) {
 #pragma unroll
     for (int ch = 0; ch < kSlide; ++ch)
 #pragma unroll
@@ -687,7 +809,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) r0[ch][kd] = row_frag(rkr, lc[kSlide + ch], kd);
   }
-  if constexpr (P2C) {
+  if constexpr (MP) {
 #pragma unroll
     for (int u = 0; u < PU; ++u)
 #pragma unroll
@@ -710,12 +832,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   u32x4_t pk1[NCH];
   u32x4_t pv1[NVB];
   uint8_t pmask1 = 0;
-  F crow1[C2P && kEarlyTile1 ? kSlide : 1][KD];
+  F crow1[MC && kEarlyTile1 ? kSlide : 1][KD];
   if constexpr (kEarlyTile1) {
     prefetch_k_into(jstart + BN, pk1, pmask1);
     if constexpr (VBUFS == 2) prefetch_v_into(jstart + BN, pv1);
   }
-  if constexpr (C2P && kEarlyTile1) {
+  if constexpr (MC && kEarlyTile1) {
 #pragma unroll
     for (int ch = 0; ch < kSlide; ++ch)
 #pragma unroll
@@ -742,7 +864,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   const int jend = SPLIT ? min(klast + 1, jstart + p.split_tiles * BN) : klast + 1;
 
   // ---- prologue: carried c2p chunks of tile 0 ----
-  if constexpr (C2P) {
+  if constexpr (MC) {
 #pragma unroll
     for (int ch = 0; ch < kCarry; ++ch)
 #pragma unroll
@@ -768,7 +890,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
       for (int n = 0; n < NVB; ++n) pv[n] = pv1[n];
     }
-    if constexpr (C2P) {
+    if constexpr (MC) {
 #pragma unroll
       for (int ch = 0; ch < kSlide; ++ch) {
 #pragma unroll
@@ -818,6 +940,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       stage_v(Vt);
       prefetch_v(SPLIT && jn >= jend ? L : jn);
     }
+    // Table form: windows of this tile into LDS, lookups of the next.
+    table_store();
+    table_lookups(jn);
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
     f32x4_t sc[KB][kQB];
@@ -860,7 +985,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           for (int kd = 0; kd < KD; ++kd) acc = M::run(kf[kd], qf[qb][kd], acc);
           sc[kb][qb] = acc;
         }
-        if constexpr (P2C) {
+        if constexpr (MP) {
           // Keys of block kb meet window indices [BN - 16(kb+1), BM + BN - 2 - 16kb]:
           // chunks outside [KB-1-kb, (BM+BN-2)/16 - kb] are read by no score element.
 #pragma unroll
@@ -907,7 +1032,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           for (int kd = 0; kd < KD; ++kd) acc = M::run(kf[kd], qf[qb][kd], acc);
           sc[kb][qb] = acc;
         }
-        if constexpr (P2C) {
+        if constexpr (MP) {
 #pragma unroll
           for (int u = 0; u < PU; ++u) {
             const int pc = wave + kWaves * u;
@@ -920,7 +1045,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
       }
     }
-    if constexpr (P2C) {
+    if constexpr (MP) {
       // Next tile's p2c rows: shift the kept chunks up by 4, load the new one.
 #pragma unroll
       for (int u = PU - 1; u > 0; --u)
@@ -993,6 +1118,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       }
     }
 
+    table_load(jn);
+
     // ---- masking (wavefront-uniform slow path: tiles with a padded key or past L) ----
     // Every row drops the padded keys.  That is the rule for kept queries; the
     // other rows are never stored from the accumulators (a padded query in
@@ -1064,7 +1191,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         return __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
       }
     };
-    constexpr bool kVtEarly = D >= 128 && !SPLIT && C2P && P2C;
+    constexpr bool kVtEarly = D >= 128 && !SPLIT && !TABLE && C2P && P2C;
     QF vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
     if constexpr (kVtEarly) {
 #pragma unroll
@@ -1365,7 +1492,7 @@ __global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __res
   *reinterpret_cast<Quad<T>*>(out + row * D + d0) = q;
 }
 
-template <typename T, int D, int QW, bool C2P, bool P2C, bool FAST = false>
+template <typename T, int D, int QW, bool C2P, bool P2C, bool FAST = false, bool TABLE = false>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
   constexpr int VB = rel_v_buffers<T, D, QW>();
@@ -1375,8 +1502,8 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
   // 16 at d = 128); fp32 never splits.
-  constexpr bool kSplitBuilt = sizeof(T) == 2 && ((D >= 128) || QW == 32);
-  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false, FAST>;
+  constexpr bool kSplitBuilt = sizeof(T) == 2 && ((D >= 128) || QW == 32) && !TABLE;
+  constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false, FAST, TABLE>;
   if (prm.splits < 1) prm.splits = 1;
   if (!kSplitBuilt && prm.splits > 1) return DFLASH_ERR_SHAPE;
   hipError_t err = hipSuccess;
@@ -1411,6 +1538,14 @@ template <typename T, int D, int QW, bool FAST = false>
 int rel_modes_qw(const RelParams& prm, hipStream_t stream) {
   if constexpr (sizeof(T) == 4 && !FAST) {
     if (prm.fast) return rel_modes_qw<T, D, QW, true>(prm, stream);
+  }
+  // Table form: the default tile of each head dim, 16-bit or IEEE fp32.
+  if constexpr (!FAST && QW == (D >= 128 ? 16 : 32)) {
+    if (prm.table) {
+      if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true, false, true>(prm, stream);
+      if (prm.has_c2p) return launch_rel<T, D, QW, true, false, false, true>(prm, stream);
+      if (prm.has_p2c) return launch_rel<T, D, QW, false, true, false, true>(prm, stream);
+    }
   }
   if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true, FAST>(prm, stream);
   if (prm.has_c2p) return launch_rel<T, D, QW, true, false, FAST>(prm, stream);

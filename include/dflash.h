@@ -63,7 +63,11 @@ extern "C" {
  *                       entry point runs IEEE fp32 MFMA for either value (the
  *                       fast fp32 form is built for dflash_attention_rel_fwd).
  * B == 0 is a no-op that returns 0 (pointers are not inspected), like the
- * reference's launch over an empty grid.
+ * reference's launch over an empty grid.  query, key, value and out must be
+ * 16-byte aligned (DFLASH_ERR_ALIGN); one (b, h) slice of a table,
+ * L * S * sizeof(element), must stay below 2^31 bytes (DFLASH_ERR_TOO_LARGE).
+ * Entries of delta_to_local outside [0, S) give undefined values but no
+ * access outside the (b, h) slice of a table.
  */
 DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const void* value,
                          const void* c2p, const void* p2c, const int32_t* delta_to_local,

@@ -162,6 +162,49 @@ def test_table_kernel_matches_reference(dtype, mode):
     _check(out, *args, has_c2p, has_p2c, "table")
 
 
+@pytest.mark.parametrize("dtype", list(DTYPES))
+@pytest.mark.parametrize("dim,heads", [(32, 4), (128, 2)])
+@pytest.mark.parametrize("mode", ["both", "c2p", "p2c"])
+def test_table_kernel_head_dims(dtype, dim, heads, mode):
+    # The table form of the d = 32 and d = 128 instances (windows read from the
+    # [B, H, L, S] tables instead of computed).
+    has_c2p, has_p2c = MODES[mode]
+    args = _inputs(2, heads, 200, dim, DTYPES[dtype], "right", seed=dim + heads + 1)
+    out = _run_table(*args, has_c2p, has_p2c)
+    _check(out, *args, has_c2p, has_p2c, f"table d={dim} {mode}")
+
+
+@pytest.mark.parametrize("length", [1, 2, 63, 64, 65, 129, 257, 513, 1024])
+@pytest.mark.parametrize("dtype", ["fp16", "fp32"])
+def test_table_kernel_lengths(length, dtype):
+    # Partial tiles, windows reaching past both ends of the tables, L > 512
+    # (S = 512: deltas beyond the bucket range share slots).
+    args = _inputs(2, 2, length, 64, DTYPES[dtype], "right", seed=length + 3)
+    out = _run_table(*args, True, True)
+    _check(out, *args, True, True, f"table L={length}")
+
+
+@pytest.mark.parametrize("pattern", ["left", "heavy", "all", "middle", "holes", "boundary"])
+@pytest.mark.parametrize("dim,heads", [(64, 3), (128, 2)])
+def test_table_kernel_mask_patterns(pattern, dim, heads):
+    args = _inputs(10, heads, 384, dim, torch.float16, pattern, seed=dim + 13)
+    out = _run_table(*args, True, True)
+    _check(out, *args, True, True, f"table {pattern} d={dim}")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_table_kernel_accepts_any_lut(dtype):
+    """The table form reads each window value through delta_to_local: any slot
+    table works, as in the reference kernel (kernel.py:228-233)."""
+
+    args = list(_inputs(3, 2, 200, 64, DTYPES[dtype], "right", seed=23))
+    slots = args[3].shape[1]
+    gen = torch.Generator().manual_seed(5)
+    args[5] = torch.randint(0, slots, (2 * 200 - 1,), generator=gen, dtype=torch.int32).cuda()
+    out = _run_table(*args, True, True)
+    _check(out, *args, True, True, "table random lut")
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("pattern", ["right", "none"])
 def test_c2_full_size(dtype, pattern):
