@@ -660,6 +660,10 @@ def main() -> int:
                              "(B=16 L=384 H=16 d=32), c5_d128 (B=16 L=512 H=8 d=128); the C5 "
                              "shapes mix the boundary valid lengths")
     parser.add_argument("--kernel-dtype", choices=sorted(KERNEL_DTYPES), default="fp16")
+    parser.add_argument("--table-only", action="store_true",
+                        help="launch only the reference-contract kernel (dflash_attention_fwd) on "
+                             "precomputed C2 fp16 c2p/p2c tables: the clock ramp, then --steps "
+                             "launches (profiling driver)")
     parser.add_argument("--tile-sweep", action="store_true",
                         help="fused op over batch sizes for d=32/64/128 (tile-table evidence)")
     parser.add_argument("--encoder-only", action="store_true",
@@ -724,6 +728,15 @@ def main() -> int:
     if args.tile_sweep:
         print(json.dumps({"tile_sweep": "fused fp16 c2p|p2c, unsplit, us",
                           "rows": bench_tile_sweep(args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.table_only:
+        call = table_call(c2_inputs(torch.float16, padded=False), precomputed=True)
+        ramp_clocks(call)
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            call()
+        torch.cuda.synchronize()
+        log(f"launched the reference-contract C2 kernel {args.steps} times")
         return 0
     if args.kernel_only:
         dtype, strict = KERNEL_DTYPES[args.kernel_dtype]
