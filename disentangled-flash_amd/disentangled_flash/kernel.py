@@ -64,6 +64,8 @@ def deberta_attention(
     output is ``[B, L, H*d]`` in the input dtype.
     """
 
+    _check_table_inputs(query, key, value, c2p, p2c, delta_to_local, attention_mask, num_heads,
+                        sequence_length, active_slots, has_c2p, has_p2c)
     lib = _lib.load()
     batch, _, length, head_dim = query.shape
     out = torch.empty(
@@ -177,6 +179,53 @@ def deberta_attention_rel(
 
 
 _SPLIT_PLANS: dict[tuple, tuple[int, int]] = {}
+
+
+def _check_table_inputs(query, key, value, c2p, p2c, delta_to_local, attention_mask, num_heads,
+                        sequence_length, active_slots, has_c2p, has_p2c) -> None:
+    """Host checks of ``deberta_attention``'s tensors before anything is launched.
+
+    The kernel addresses Q/K/V as ``[B, H, L, d]`` and each table as
+    ``[B, H, L, S]`` from the integers given here, so a tensor of another shape,
+    layout or dtype would be read out of bounds or as garbage.
+    """
+
+    if query.dim() != 4:
+        raise ValueError(f"query must be [B, H, L, d], got shape {tuple(query.shape)}")
+    batch, heads, length, head_dim = query.shape
+    if heads != num_heads or length != sequence_length:
+        raise ValueError(f"query shape {tuple(query.shape)} does not match num_heads={num_heads}, "
+                         f"sequence_length={sequence_length}")
+    if query.dtype not in SUPPORTED_DTYPES:
+        raise TypeError(f"query dtype {query.dtype} is not fp16, bf16 or fp32")
+    device = query.device
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if t.shape != query.shape or t.dtype != query.dtype or t.device != device:
+            raise ValueError(f"{name} must match query: [B, H, L, d] {tuple(query.shape)}, "
+                             f"{query.dtype}, {device}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    for name, table, used in (("c2p", c2p, has_c2p), ("p2c", p2c, has_p2c)):
+        if not used:
+            continue
+        if table.shape != (batch, heads, length, active_slots):
+            raise ValueError(f"{name} must be [B, H, L, S] = {(batch, heads, length, active_slots)}, "
+                             f"got {tuple(table.shape)}")
+        if table.dtype != query.dtype or table.device != device or not table.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {query.dtype} tensor on {device}")
+    if delta_to_local.dtype != torch.int32 or delta_to_local.dim() != 1:
+        raise TypeError("delta_to_local must be a 1-D int32 tensor")
+    if length > 0 and delta_to_local.numel() != 2 * length - 1:
+        raise ValueError(f"delta_to_local has {delta_to_local.numel()} entries, expected "
+                         f"2L-1 = {2 * length - 1}")
+    if not delta_to_local.is_contiguous() or delta_to_local.device != device:
+        raise ValueError("delta_to_local must be contiguous and on the query device")
+    if attention_mask.shape != (batch, length):
+        raise ValueError(f"attention_mask shape {tuple(attention_mask.shape)} does not match "
+                         f"[{batch}, {length}]")
+    if attention_mask.element_size() != 1 or not attention_mask.is_contiguous() or (
+            attention_mask.device != device):
+        raise ValueError("attention_mask must be a contiguous bool/uint8 tensor on the query device")
 
 
 def _check_rel_inputs(qkv, pos_key, pos_query, delta_to_local, attention_mask, num_heads,

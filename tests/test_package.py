@@ -207,6 +207,46 @@ def test_hip_module_validation_errors_on_cpu():
                               False, key_splits=-1)
 
 
+def test_table_op_checks_its_tensors_before_launching():
+    """deberta_attention (the reference op's contract) rejects tensors whose shape,
+    layout or dtype differ from what the kernel will address, on the host."""
+
+    from disentangled_flash.kernel import deberta_attention
+
+    b, h, length, d, s = 2, 3, 5, 32, 9
+    q, k, v = (torch.zeros(b, h, length, d, dtype=torch.float16) for _ in range(3))
+    c2p = torch.zeros(b, h, length, s, dtype=torch.float16)
+    lut = torch.zeros(2 * length - 1, dtype=torch.int32)
+    mask = torch.ones(b, length, dtype=torch.bool)
+
+    def call(**over):
+        args = dict(query=q, key=k, value=v, c2p=c2p, p2c=c2p, delta_to_local=lut,
+                    attention_mask=mask, num_heads=h, sequence_length=length, active_slots=s,
+                    score_scale_log2=1.0, has_c2p=True, has_p2c=True, is_bf16=False,
+                    is_fp32=False, strict_fp32=True)
+        args.update(over)
+        return deberta_attention(*args.values())
+
+    with pytest.raises(ValueError, match="c2p must be"):
+        call(c2p=torch.zeros(b, h, length, s - 1, dtype=torch.float16))
+    with pytest.raises(ValueError, match="p2c must be"):
+        call(p2c=c2p.float())
+    with pytest.raises(ValueError, match="key must be contiguous"):
+        call(key=torch.zeros(b, h, d, length, dtype=torch.float16).transpose(-1, -2))
+    with pytest.raises(ValueError, match="value must match"):
+        call(value=torch.zeros(b, h, length + 1, d, dtype=torch.float16))
+    with pytest.raises(ValueError, match="does not match num_heads"):
+        call(num_heads=h + 1)
+    with pytest.raises(TypeError, match="int32"):
+        call(delta_to_local=lut.long())
+    with pytest.raises(ValueError, match="2L-1"):
+        call(delta_to_local=lut[:-1])
+    with pytest.raises(ValueError, match="attention_mask shape"):
+        call(attention_mask=torch.ones(b, length + 1, dtype=torch.bool))
+    with pytest.raises(TypeError, match="not fp16"):
+        call(query=q.double(), key=k.double(), value=v.double())
+
+
 def _tiny_deberta(layers=2, conv=3):
     from transformers import DebertaV2Config, DebertaV2Model
 
