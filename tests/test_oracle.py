@@ -222,3 +222,17 @@ def test_float64_buckets_differ_from_float32_somewhere():
     span = np.arange(-8191, 8192)
     ref = make_log_bucket_position(torch.from_numpy(span), 256, 512).to(torch.long).numpy()
     assert np.array_equal(ref, log_bucket(span, 256, 512, dtype=np.float64))
+
+
+def test_reference_scale_casts_like_the_original_path():
+    """Known answers for the original path's scale quirk: sqrt(float32(d) * f) cast to
+    the activation dtype before dividing (``_reference.py:161-162,285``).  For d = 64,
+    f = 3 the exact value 13.8564... becomes 13.859375 in fp16 and 13.875 in bf16."""
+
+    import torch
+
+    assert reference_scale(64, 3) == np.float32(np.sqrt(np.float32(192.0)))
+    assert reference_scale(64, 3, np.float16) == 13.859375
+    bf16 = float(torch.tensor(reference_scale(64, 3), dtype=torch.float32).to(torch.bfloat16))
+    assert bf16 == 13.875
+    assert reference_scale(64, 1, np.float16) == 8.0  # exact: no rounding at f = 1
