@@ -230,6 +230,27 @@ int scratch_address(void** ptr) {
   return DFLASH_OK;
 }
 
+// In-flight guard of the scratch, per device: the stream of the last call
+// that used it and an event recorded after that call's kernels.  A call from
+// another stream while that event is still pending would overwrite partial
+// rows the earlier call has not merged yet, so it is refused
+// (DFLASH_ERR_BUSY).  Calls on one stream are ordered by the stream and always
+// pass.  While a stream is being captured into a HIP graph nothing is
+// recorded or queried (a captured launch runs at replay time, which only the
+// caller orders).
+struct ScratchUse {
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool pending = false;
+};
+ScratchUse g_scratch_use[kMaxDevices];
+
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &status) == hipSuccess &&
+         status != hipStreamCaptureStatusNone;
+}
+
 }  // namespace
 
 extern "C" {
@@ -301,14 +322,38 @@ int dflash_attention_rel_fwd_noalloc(const void* query, const void* key, const v
   const size_t need = rel_attention_workspace_bytes(count, B, H, L, D);
   if (need > kScratchBytes) return DFLASH_ERR_SCRATCH;
   void* ws = nullptr;
-  if (count > 1) {
-    const int rc = scratch_address(&ws);
-    if (rc != DFLASH_OK) return rc;
+  if (count <= 1) {  // no partial rows: the scratch is not touched
+    return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
+                       delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
+                       has_c2p, has_p2c, dtype, strict_fp32, 1, nullptr, 0, stream);
   }
-  return rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
-                     delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
-                     has_c2p, has_p2c, dtype, strict_fp32, count, ws, count > 1 ? kScratchBytes : 0,
-                     stream);
+  int rc = scratch_address(&ws);
+  if (rc != DFLASH_OK) return rc;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return static_cast<int>(err);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const bool capturing = stream_capturing(hs);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  ScratchUse& use = g_scratch_use[dev];
+  if (!capturing && use.pending && use.stream != hs) {
+    err = hipEventQuery(use.done);
+    if (err == hipErrorNotReady) return DFLASH_ERR_BUSY;
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
+  rc = rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
+                   delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
+                   has_c2p, has_p2c, dtype, strict_fp32, count, ws, kScratchBytes, stream);
+  if (rc != DFLASH_OK || capturing) return rc;
+  if (!use.done) {
+    err = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
+  err = hipEventRecord(use.done, hs);
+  if (err != hipSuccess) return static_cast<int>(err);
+  use.stream = hs;
+  use.pending = true;
+  return DFLASH_OK;
 }
 
 size_t dflash_attention_rel_noalloc_scratch_bytes(void) { return kScratchBytes; }
@@ -331,6 +376,9 @@ const char* dflash_error_string(int code) {
       return "launch grid exceeds the device limit";
     case DFLASH_ERR_WORKSPACE:
       return "workspace smaller than dflash_attention_rel_split_plan reports";
+    case DFLASH_ERR_BUSY:
+      return "the static scratch is in use by a call on another stream that has not "
+             "completed (dflash_attention_rel_fwd_noalloc)";
     case DFLASH_ERR_SCRATCH:
       return "the split workspace this shape needs exceeds the library's static scratch "
              "(dflash_attention_rel_noalloc_scratch_bytes)";

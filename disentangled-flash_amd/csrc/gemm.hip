@@ -437,7 +437,9 @@ template <typename T, int EPI>
 int pick_config(const GemmArgs& args, int config, hipStream_t stream) {
   const bool wide_ok = args.N % CfgWide::BN == 0;
   const bool pair_ok = args.N % CfgPair::BN == 0;
-  if (config == 0) {
+  if (config == 0 && !wide_ok && !pair_ok) {
+    config = 5;  // N % 64 == 0 only: the 64 x 64 tiles at every row count
+  } else if (config == 0) {
     config = (wide_ok && !(EPI == kEpiBiasGelu && pair_ok)) ? 3 : 2;
     // Few rows: when the 256-row grid would give fewer tiles than half the CUs,
     // the 64-row forms (four times the tiles) are faster on the device, 64 x 64

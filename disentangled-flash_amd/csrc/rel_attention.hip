@@ -508,11 +508,14 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   }
   TW tcv[TC_N];
   TW tpv[TP_N];
-  auto load_tw = [](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) -> TW {
+  // The whole byte offset goes in voffset: the range check of a raw buffer
+  // covers voffset (plus the instruction offset) but not soffset, so a row
+  // past L must be addressed through voffset to read as zero.
+  auto load_tw = [](__amdgpu_buffer_rsrc_t r, uint32_t voff) -> TW {
     if constexpr (sizeof(T) == 2) {
-      return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+      return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
     } else {
-      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
     }
   };
   // Slots of the windows of the tile at key offset j0.
@@ -538,7 +541,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
                               static_cast<uint32_t>(i0w + tc_q[pp]) * row_bytes;
 #pragma unroll
         for (int m = 0; m < TC_N / TC_P; ++m)
-          tcv[pp + TC_P * m] = load_tw(rtc, voff, static_cast<uint32_t>(m * TC_R) * row_bytes);
+          tcv[pp + TC_P * m] = load_tw(rtc, voff + static_cast<uint32_t>(m * TC_R) * row_bytes);
       }
     }
     if constexpr (TP) {
@@ -548,7 +551,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
                               static_cast<uint32_t>(j0 + tp_j[pp]) * row_bytes;
 #pragma unroll
         for (int m = 0; m < TP_N / TP_P; ++m)
-          tpv[pp + TP_P * m] = load_tw(rtp, voff, static_cast<uint32_t>(m * TP_R) * row_bytes);
+          tpv[pp + TP_P * m] = load_tw(rtp, voff + static_cast<uint32_t>(m * TP_R) * row_bytes);
       }
     }
   };

@@ -19,7 +19,7 @@ from pathlib import Path
 import torch  # noqa: F401  (load torch's HIP runtime first)
 
 LIBRARY_NAME = "libdflash.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_CODES = {
     torch.float16: 0,
@@ -148,6 +148,14 @@ def check(code: int, what: str) -> None:
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
+_PLAIN_TENSORS = (torch.Tensor, torch.nn.Parameter)
+
+try:
+    from torch.utils._python_dispatch import _get_current_dispatch_mode as _get_dispatch_mode
+except ImportError:  # pragma: no cover - older torch
+    def _get_dispatch_mode():
+        return None
+
 
 def current_stream_handle(device: torch.device) -> int:
     """The HIP stream torch launches on for ``device`` (raw handle)."""
@@ -173,8 +181,16 @@ def hip_op(name: str):
 
         @functools.wraps(impl)
         def call(*args, **kwargs):
-            if torch.compiler.is_compiling():
+            # Through the custom op when tracing (torch.compile, export,
+            # make_fx), under any dispatch mode (FakeTensorMode, opcheck) or
+            # with a tensor that is not a plain CUDA tensor, so that the
+            # registered fake runs instead of a data_ptr() of a fake tensor.
+            if torch.compiler.is_compiling() or _get_dispatch_mode() is not None:
                 return op(*args, **kwargs)
+            for a in args:
+                if isinstance(a, torch.Tensor) and (
+                        type(a) not in _PLAIN_TENSORS or a.device.type != "cuda"):
+                    return op(*args, **kwargs)
             return impl(*args, **kwargs)
 
         call.register_fake = op.register_fake

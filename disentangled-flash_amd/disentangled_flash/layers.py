@@ -182,6 +182,17 @@ def linear_epilogue(
     n = weight.shape[0]
     rows = x.numel() // k if k else 0
     out = x.new_empty(x.shape[:-1] + (n,))
+    if int(epilogue) == GEMM_BIAS_ADD:
+        # The kernel reads rows * n elements of the residual in the output dtype.
+        if residual is None:
+            raise ValueError("linear_epilogue: GEMM_BIAS_ADD needs a residual")
+        if residual.shape != out.shape:
+            raise ValueError(f"linear_epilogue: residual shape {tuple(residual.shape)} "
+                             f"!= output shape {tuple(out.shape)}")
+        if residual.dtype != x.dtype or residual.device != x.device:
+            raise ValueError("linear_epilogue: residual must have the input's dtype and device")
+        if not residual.is_contiguous():
+            raise ValueError("linear_epilogue: residual must be contiguous")
     code = lib.dflash_linear_fwd(
         x.data_ptr(), weight.data_ptr(), bias.data_ptr(),
         residual.data_ptr() if residual is not None else None, out.data_ptr(), rows, n, k,

@@ -6,10 +6,10 @@ the device, never on layer weights, so one cache serves every encoder layer.
 ``compact(L)`` returns the sorted set of relative-embedding rows ("active
 slots") that an ``L``-token sequence can touch and an int32 lookup table
 ``delta_to_local[i - j + L - 1]`` giving the position of ``slot(i - j)`` inside
-that set.  Because the bucket function is monotone in ``i - j``, any contiguous
-range of deltas maps to a contiguous range of local slots; the fused HIP kernel
-relies on this to compute relative scores for a tile from a contiguous window of
-projected position rows.
+that set.  The fused HIP kernel reads this table for every delta of a tile's
+window and gathers the projected position row of each delta, so it accepts any
+table (monotone or not); the log-bucket tables built here happen to be monotone
+in ``i - j``.
 
 ``dense(L)`` adds the ``[1, 1, L, L]`` int64 gather map that the unfused
 PyTorch path uses.

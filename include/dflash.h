@@ -25,7 +25,7 @@ extern "C" {
 
 #define DFLASH_API __attribute__((visibility("default")))
 
-#define DFLASH_ABI_VERSION 6
+#define DFLASH_ABI_VERSION 7
 
 #define DFLASH_DTYPE_FP16 0
 #define DFLASH_DTYPE_BF16 1
@@ -40,6 +40,7 @@ extern "C" {
 #define DFLASH_ERR_TOO_LARGE (-6)
 #define DFLASH_ERR_WORKSPACE (-7)
 #define DFLASH_ERR_SCRATCH (-8)
+#define DFLASH_ERR_BUSY (-9)
 
 /* Activation codes of the ConvLayer tail (the module's conv_act). */
 #define DFLASH_ACT_GELU 0 /* exact erf form, Hugging Face ACT2FN["gelu"] */
@@ -170,10 +171,14 @@ DFLASH_API int dflash_attention_rel_fwd_split(const void* query, const void* key
  * that count exceeds the scratch.  With splits = 0 on a 256-CU MI355X the
  * plan never needs more than 8.7 MB, so only forced counts on large shapes
  * are refused.
- * All calls on one GPU share that GPU's scratch: calls that overlap on one
- * GPU (on different streams, or from different host threads) race and give
- * undefined results.  The scratch keeps the last call's contents; every call
- * writes all the partial rows it reads, so nothing needs clearing.
+ * All calls on one GPU share that GPU's scratch.  Calls on one stream are
+ * ordered by it.  A split call issued from another stream while the last split
+ * call's kernels are still pending returns DFLASH_ERR_BUSY and launches nothing
+ * (the library records an event after each split call and queries it).  While
+ * the stream is being captured into a HIP graph nothing is recorded or checked:
+ * replays of graphs that use the scratch must not overlap each other or another
+ * split call on the same GPU.  The scratch keeps the last call's contents; every
+ * call writes all the partial rows it reads, so nothing needs clearing.
  */
 DFLASH_API int dflash_attention_rel_fwd_noalloc(const void* query, const void* key,
                                                 const void* value, int64_t stride_b,
@@ -257,8 +262,10 @@ DFLASH_API int dflash_conv_layer_tail_fwd(const void* z, int z_dtype, const void
  *   bias     : [N]; residual: [M, N] row-major (DFLASH_GEMM_BIAS_ADD only, else may be NULL)
  *   y        : [M, N] row-major
  *   dtype    : fp16 or bf16 (fp32 is not supported: DFLASH_ERR_DTYPE)
- * N must be a multiple of 128 or 192 and K of 32 (DFLASH_ERR_SHAPE otherwise;
- * every projection of DeBERTa base/large/xlarge qualifies); x, weight, residual, y
+ * N must be a multiple of 64 and K of 32 (DFLASH_ERR_SHAPE otherwise; every
+ * projection of DeBERTa base/large/xlarge qualifies; the automatic configuration
+ * runs the 64 x 64 tiles when N is a multiple of neither 128 nor 192, at any M);
+ * x, weight, residual, y
  * 16-byte aligned, bias 8-byte aligned.  M == 0 is a no-op.
  *   epilogue : the code above in bits 0-7; bits 8 and up select a tile
  *              configuration (0 = automatic by N and epilogue): 1 = 256 x 192

@@ -81,7 +81,7 @@ def _check(y, ref, lin, acc, dtype, epilogue):
 @pytest.mark.parametrize("epilogue", [0, 1, 2], ids=["bias", "gelu", "add"])
 @pytest.mark.parametrize("shape", [(16384, 768, 2304), (16384, 768, 3072), (4096, 3072, 768),
                                    (300, 64, 384), (1, 32, 192), (257, 1536, 4608),
-                                   (513, 96, 640)],
+                                   (513, 96, 640), (16384, 64, 320)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_linear_matches_float64(dtype, epilogue, shape):
     m, k, n = shape
@@ -90,7 +90,9 @@ def test_linear_matches_float64(dtype, epilogue, shape):
     for name, config in CONFIGS.items():
         if config in (1, 3) and n % 192 or config in (2, 4) and n % 128:
             continue
-        if config != 5 and n % 128 and n % 192:
+        # Widths that fit neither 128 nor 192 run the 64 x 64 tiles, forced or
+        # automatic (at any row count).
+        if config not in (0, 5) and n % 128 and n % 192:
             continue
         code, y = _run(x, w, b, r if epilogue == 2 else None, epilogue, config)
         assert code == 0, (name, code)

@@ -219,3 +219,38 @@ def test_conv_layer_tail_rejects_bad_arguments():
     assert call(hidden=6) == -2     # hidden not a multiple of 4
     assert call(z_dtype=1) == -4    # taps neither fp32 nor the dtype
     assert call(batch=0) == 0       # empty batch is a no-op
+
+
+def test_hip_ops_run_their_fakes_under_fake_tensor_mode():
+    """Under FakeTensorMode (as in non-strict export or opcheck) the HIP ops go
+    through their registered fake implementations, not the C ABI."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from disentangled_flash import layers
+
+    with FakeTensorMode():
+        x = torch.empty(4, 256, 768, device="cuda", dtype=torch.float16)
+        w = torch.empty(2304, 768, device="cuda", dtype=torch.float16)
+        b = torch.empty(2304, device="cuda", dtype=torch.float16)
+        y = layers.linear_epilogue(x, w, b, None, layers.GEMM_BIAS)
+        assert y.shape == (4, 256, 2304) and y.dtype == torch.float16
+
+
+def test_linear_epilogue_checks_the_residual():
+    from disentangled_flash import layers
+
+    x = torch.randn(64, 256, device="cuda", dtype=torch.float16)
+    w = torch.randn(128, 256, device="cuda", dtype=torch.float16) / 16
+    b = torch.randn(128, device="cuda", dtype=torch.float16)
+    good = torch.randn(64, 128, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError, match="needs a residual"):
+        layers.linear_epilogue(x, w, b, None, layers.GEMM_BIAS_ADD)
+    with pytest.raises(ValueError, match="shape"):
+        layers.linear_epilogue(x, w, b, good[:32], layers.GEMM_BIAS_ADD)
+    with pytest.raises(ValueError, match="dtype"):
+        layers.linear_epilogue(x, w, b, good.float(), layers.GEMM_BIAS_ADD)
+    with pytest.raises(ValueError, match="contiguous"):
+        layers.linear_epilogue(x, w, b, good.t().contiguous().t(), layers.GEMM_BIAS_ADD)
+    y = layers.linear_epilogue(x, w, b, good, layers.GEMM_BIAS_ADD)
+    ref = (F.linear(x.double(), w.double(), b.double()).half().double() + good.double())
+    assert (y.double() - ref).abs().max().item() < 2e-2

@@ -256,6 +256,67 @@ def test_c3_sweep_cells_fp16(base_encoder, shape):
     assert err <= 1.5 * ref_err + TOL[torch.float16]
 
 
+C3_BATCHES = (1, 8, 16, 32)
+C3_LENGTHS = (16, 32, 64, 128, 256, 384, 512)
+
+
+def _sweep(base, torch_dtype, cells):
+    """Every (B, L) cell against HF fp32 and HF in the dtype; three models built once.
+
+    The HIP encoder is prepared with all the cells' lengths as buckets, as
+    ``optimize_deberta(sequence_lengths=...)`` is for the C3 sweep.
+    """
+
+    from disentangled_flash import enable_deberta_inference
+
+    lengths = sorted({length for _, length in cells})
+    results = []
+    with torch.inference_mode():
+        ref32 = copy.deepcopy(base).to("cuda", torch.float32).encoder
+        ref = copy.deepcopy(base).to("cuda", torch_dtype).encoder
+        fast = enable_deberta_inference(copy.deepcopy(base).to("cuda", torch_dtype),
+                                        backend="hip", sequence_lengths=lengths).encoder
+        for batch, length in cells:
+            hidden, mask = _encoder_inputs(batch, length, base.config.hidden_size,
+                                           seed=batch + length)
+            hidden, mask = hidden.cuda(), mask.cuda()
+            exact = ref32(hidden.float(), mask, output_hidden_states=False).last_hidden_state
+            same = ref(hidden.to(torch_dtype), mask, output_hidden_states=False).last_hidden_state
+            fast.activate_shape(length)  # the prepared bucket of this cell
+            got = fast(hidden.to(torch_dtype), mask, output_hidden_states=False).last_hidden_state
+            valid = mask.bool()[..., None]
+            err = ((got.float() - exact).abs() * valid).max().item()
+            ref_err = ((same.float() - exact).abs() * valid).max().item()
+            print(f"C3 {torch_dtype} B={batch} L={length}: hip-vs-HF-fp32 {err:.3e}, "
+                  f"HF-in-dtype-vs-HF-fp32 {ref_err:.3e}", flush=True)
+            results.append((batch, length, err, ref_err))
+    del ref32, ref, fast
+    torch.cuda.empty_cache()
+    return results
+
+
+def test_c3_full_sweep_fp16(base_encoder):
+    """All 28 cells of the C3 sweep, B in {1, 8, 16, 32} x L in {16 .. 512}, fp16, under
+    the encoder rule (within 1.5x HF fp16's own error plus the attention tolerance)."""
+
+    cells = [(b, length) for length in C3_LENGTHS for b in C3_BATCHES]
+    results = _sweep(base_encoder, torch.float16, cells)
+    assert len(results) == 28
+    bad = [(b, length, err, ref_err) for b, length, err, ref_err in results
+           if not err <= 1.5 * ref_err + TOL[torch.float16]]
+    assert not bad, bad
+
+
+def test_c3_sweep_bf16_long_buckets(base_encoder):
+    """bf16 at the long buckets, B in {1, 32} x L in {384, 512}."""
+
+    cells = [(b, length) for length in (384, 512) for b in (1, 32)]
+    results = _sweep(base_encoder, torch.bfloat16, cells)
+    bad = [(b, length, err, ref_err) for b, length, err, ref_err in results
+           if not err <= 1.5 * ref_err + TOL[torch.bfloat16]]
+    assert not bad, bad
+
+
 def test_12_layer_encoder_fast_fp32(base_encoder):
     """fp32_precision="fast" through the 12-layer encoder, against HF fp32."""
 

@@ -122,3 +122,42 @@ def test_no_alloc_without_split_and_refusal():
     assert b"scratch" in lib.dflash_error_string(code)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all()), "a refused call must launch nothing"
+
+
+def test_no_alloc_refuses_overlap_from_another_stream():
+    """A split call from a second stream while the first stream's call is pending
+    returns DFLASH_ERR_BUSY and launches nothing; once it has completed, or on the
+    same stream, calls pass and match the workspace entry point."""
+    from disentangled_flash import _lib
+
+    lib = _lib.load()
+    inp = _inputs(1, 12, 512, 64, torch.float16, 6, lengths=[512])
+    want, count = _with_workspace(lib, inp, 0)
+    assert count > 1, "the case must exercise the split form (scratch in use)"
+    first = torch.empty_like(want)
+    blocked = torch.full_like(want, 7.0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        # Keep s1 busy (a bounded spin kernel) so that its split call is still
+        # pending when s2 asks for the scratch.
+        torch.cuda._sleep(50_000_000)
+        assert lib.dflash_attention_rel_fwd_noalloc(*_common_args(inp, first), 0,
+                                                    s1.cuda_stream) == 0
+        # Same stream: ordered, so it passes.
+        again = torch.empty_like(want)
+        assert lib.dflash_attention_rel_fwd_noalloc(*_common_args(inp, again), 0,
+                                                    s1.cuda_stream) == 0
+    code = lib.dflash_attention_rel_fwd_noalloc(*_common_args(inp, blocked), 0, s2.cuda_stream)
+    print(f"second stream while the first is pending: code {code}", flush=True)
+    assert code == -9
+    assert b"another stream" in lib.dflash_error_string(code)
+    s1.synchronize()
+    torch.cuda.synchronize()
+    assert bool((blocked == 7.0).all()), "a refused call must launch nothing"
+    assert torch.equal(first, want) and torch.equal(again, want)
+    # After s1 has completed, s2 may use the scratch.
+    late = torch.empty_like(want)
+    assert lib.dflash_attention_rel_fwd_noalloc(*_common_args(inp, late), 0, s2.cuda_stream) == 0
+    s2.synchronize()
+    assert torch.equal(late, want)
