@@ -259,7 +259,7 @@ struct RelLayout {
 }  // namespace
 
 template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool P2C, bool SPLIT,
-          bool FAST = false, bool TABLE = false>
+          bool FAST = false, bool TABLE = false, bool ROWSAFE = false>
 __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
   static_assert(!FAST || sizeof(T) == 4, "the bf16x3 form is for fp32 data");
   static_assert(!(TABLE && (FAST || SPLIT)), "the table form runs unsplit and in IEEE fp32");
@@ -314,8 +314,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // Key split of the split-key form (the splits of a block are neighbours).
   const int split = SPLIT ? mk % p.splits : 0;
   const int m = SPLIT ? mk / p.splits : mk;
-  const int bh = m / p.nqb;
-  const int qblk = m - bh * p.nqb;
+  const int qblk = m % p.nqb;
+  const int bh = p.bh0 + m / p.nqb;
   const int b = bh / p.H;
   const int h = bh - b * p.H;
   const int i0 = qblk * BM;
@@ -508,14 +508,27 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   }
   TW tcv[TC_N];
   TW tpv[TP_N];
-  // The whole byte offset goes in voffset: the range check of a raw buffer
-  // covers voffset (plus the instruction offset) but not soffset, so a row
-  // past L must be addressed through voffset to read as zero.
-  auto load_tw = [](__amdgpu_buffer_rsrc_t r, uint32_t voff) -> TW {
+  // A lane reads rows r0 + m TC_R of one lookup's slot.  The range check of a
+  // raw buffer covers voffset (and the instruction offset) but not soffset.
+  // The fast form puts the row step in soffset (one address register per
+  // lookup); a row past L then reads outside the (b, h) slice - inside the
+  // tensor for every slice but the last, whose query blocks and key tiles
+  // therefore run the ROWSAFE instance when L is not a multiple of the tile
+  // (see launch_rel).  ROWSAFE carries the whole offset in voffset, so rows
+  // past L read as zero; it costs address registers (spills), and runs only on
+  // that one slice.
+  auto load_tw = [](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) -> TW {
     if constexpr (sizeof(T) == 2) {
-      return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
     } else {
-      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+  };
+  auto row_load = [&](__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t step) -> TW {
+    if constexpr (ROWSAFE) {
+      return load_tw(r, voff + step, 0);
+    } else {
+      return load_tw(r, voff, step);
     }
   };
   // Slots of the windows of the tile at key offset j0.
@@ -541,7 +554,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
                               static_cast<uint32_t>(i0w + tc_q[pp]) * row_bytes;
 #pragma unroll
         for (int m = 0; m < TC_N / TC_P; ++m)
-          tcv[pp + TC_P * m] = load_tw(rtc, voff + static_cast<uint32_t>(m * TC_R) * row_bytes);
+          tcv[pp + TC_P * m] = row_load(rtc, voff, static_cast<uint32_t>(m * TC_R) * row_bytes);
       }
     }
     if constexpr (TP) {
@@ -551,7 +564,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
                               static_cast<uint32_t>(j0 + tp_j[pp]) * row_bytes;
 #pragma unroll
         for (int m = 0; m < TP_N / TP_P; ++m)
-          tpv[pp + TP_P * m] = load_tw(rtp, voff + static_cast<uint32_t>(m * TP_R) * row_bytes);
+          tpv[pp + TP_P * m] = row_load(rtp, voff, static_cast<uint32_t>(m * TP_R) * row_bytes);
       }
     }
   };
@@ -1524,8 +1537,28 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   if (prm.splits <= 1) {
     err = ensure_dynamic_lds<kernel>(static_cast<int>(LY::bytes));
     if (err != hipSuccess) return static_cast<int>(err);
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), LY::bytes,
-                       stream, prm);
+    // Table form with L not a multiple of the tiles: the last (b, h) slice,
+    // whose rows past L would read past the end of the tables, runs the
+    // ROWSAFE instance (see the kernel).
+    const int64_t groups = static_cast<int64_t>(prm.B) * prm.H;
+    const bool tail = TABLE && groups > 0 && (prm.L % LY::BM != 0 || prm.L % BN != 0);
+    const int64_t fast_blocks = tail ? blocks - prm.nqb : blocks;
+    if (fast_blocks > 0) {
+      hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(fast_blocks)), dim3(kThreads), LY::bytes,
+                         stream, prm);
+    }
+    if constexpr (TABLE) {
+      if (tail) {
+        constexpr auto safe_kernel =
+            rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false, FAST, TABLE, true>;
+        err = ensure_dynamic_lds<safe_kernel>(static_cast<int>(LY::bytes));
+        if (err != hipSuccess) return static_cast<int>(err);
+        RelParams last = prm;
+        last.bh0 = static_cast<int>(groups - 1);
+        hipLaunchKernelGGL(safe_kernel, dim3(static_cast<unsigned>(prm.nqb)), dim3(kThreads),
+                           LY::bytes, stream, last);
+      }
+    }
   }
   err = hipGetLastError();
   if (err != hipSuccess || prm.splits == 1) return static_cast<int>(err);

@@ -184,6 +184,18 @@ def test_table_kernel_lengths(length, dtype):
     _check(out, *args, True, True, f"table L={length}")
 
 
+@pytest.mark.parametrize("batch,heads,length", [(1, 1, 100), (1, 1, 64), (3, 1, 77), (1, 5, 200)])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_table_kernel_last_slice(batch, heads, length, dtype):
+    """L not a multiple of the tiles: every (b, h) slice but the last runs the
+    soffset-stepped loads, the last one (whose rows past L would leave the
+    tensor) the range-checked form; a single slice runs that form alone."""
+
+    args = _inputs(batch, heads, length, 64, DTYPES[dtype], "right", seed=length + batch)
+    out = _run_table(*args, True, True)
+    _check(out, *args, True, True, f"table last slice B={batch} H={heads} L={length}")
+
+
 @pytest.mark.parametrize("pattern", ["left", "heavy", "all", "middle", "holes", "boundary"])
 @pytest.mark.parametrize("dim,heads", [(64, 3), (128, 2)])
 def test_table_kernel_mask_patterns(pattern, dim, heads):
