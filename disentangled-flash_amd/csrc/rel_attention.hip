@@ -531,17 +531,23 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       return load_tw(r, voff, step);
     }
   };
-  // Slots of the windows of the tile at key offset j0.
+  // Slots of the windows of the tile at key offset j0.  A lookup entry
+  // outside [0, S) is clamped to S - 1: its value is undefined (as in the
+  // reference), but its offset stays inside its table row, so that with the
+  // row step in soffset (unchecked) no read leaves the tensor.
+  const uint32_t slot_max = static_cast<uint32_t>(p.S - 1);
   auto table_lookups = [&](int j0) {
     if constexpr (TC) {
 #pragma unroll
       for (int pp = 0; pp < TC_P; ++pp)
-        tc_slot[pp] = lut_load(i0w - j0 - (BN - 1) + tc_t[pp] + L - 1);
+        tc_slot[pp] = static_cast<int>(
+            min(static_cast<uint32_t>(lut_load(i0w - j0 - (BN - 1) + tc_t[pp] + L - 1)), slot_max));
     }
     if constexpr (TP) {
 #pragma unroll
       for (int pp = 0; pp < TP_P; ++pp)
-        tp_slot[pp] = lut_load(i0 - j0 - (BN - 1) + tp_t[pp] + L - 1);
+        tp_slot[pp] = static_cast<int>(
+            min(static_cast<uint32_t>(lut_load(i0 - j0 - (BN - 1) + tp_t[pp] + L - 1)), slot_max));
     }
   };
   // Window values of the tile at key offset j0 (slots from table_lookups(j0)).

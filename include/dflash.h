@@ -67,8 +67,8 @@ extern "C" {
  * reference's launch over an empty grid.  query, key, value and out must be
  * 16-byte aligned (DFLASH_ERR_ALIGN); one (b, h) slice of a table,
  * L * S * sizeof(element), must stay below 2^31 bytes (DFLASH_ERR_TOO_LARGE).
- * Entries of delta_to_local outside [0, S) give undefined values but no
- * access outside the (b, h) slice of a table.
+ * Entries of delta_to_local outside [0, S) give undefined values (they read
+ * slot S - 1); every read stays inside the c2p / p2c tensors.
  */
 DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const void* value,
                          const void* c2p, const void* p2c, const int32_t* delta_to_local,

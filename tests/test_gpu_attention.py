@@ -217,6 +217,27 @@ def test_table_kernel_accepts_any_lut(dtype):
     _check(out, *args, True, True, "table random lut")
 
 
+@pytest.mark.parametrize("length", [200, 256])
+def test_table_kernel_out_of_range_lut_entries(length):
+    """Entries outside [0, S) give undefined values (the kernel reads slot S - 1)
+    but stay inside the tables: entries of S .. L*S and negative ones, in the last
+    (b, h) slice too, finish with finite output; in-range entries are unaffected
+    where no score uses a bad entry."""
+
+    args = list(_inputs(2, 2, length, 64, torch.float16, "right", seed=29))
+    slots = args[3].shape[1]
+    gen = torch.Generator().manual_seed(7)
+    bad = torch.randint(slots, length * slots, (2 * length - 1,), generator=gen, dtype=torch.int32)
+    bad[::3] = -torch.randint(1, 1 << 30, (bad[::3].numel(),), generator=gen, dtype=torch.int32)
+    args[5] = bad.cuda()
+    out = _run_table(*args, True, True)
+    assert torch.isfinite(out).all()
+    # Clamped to S - 1: the same as a table that maps every delta to S - 1.
+    args[5] = torch.full((2 * length - 1,), slots - 1, dtype=torch.int32).cuda()
+    want = _run_table(*args, True, True)
+    assert torch.equal(out, want)
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("pattern", ["right", "none"])
 def test_c2_full_size(dtype, pattern):
