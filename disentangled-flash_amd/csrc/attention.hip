@@ -341,14 +341,14 @@ int dflash_attention_rel_fwd_noalloc(const void* query, const void* key, const v
     if (err == hipErrorNotReady) return DFLASH_ERR_BUSY;
     if (err != hipSuccess) return static_cast<int>(err);
   }
+  if (!capturing && !use.done) {  // before launching: a failure here launches nothing
+    err = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
   rc = rel_forward(query, key, value, stride_b, stride_h, stride_l, pos_key, pos_query,
                    delta_to_local, attention_mask, out, B, H, L, D, S, score_scale_log2,
                    has_c2p, has_p2c, dtype, strict_fp32, count, ws, kScratchBytes, stream);
   if (rc != DFLASH_OK || capturing) return rc;
-  if (!use.done) {
-    err = hipEventCreateWithFlags(&use.done, hipEventDisableTiming);
-    if (err != hipSuccess) return static_cast<int>(err);
-  }
   err = hipEventRecord(use.done, hs);
   if (err != hipSuccess) return static_cast<int>(err);
   use.stream = hs;
