@@ -60,9 +60,6 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
                          const uint8_t* attention_mask, void* out, int B, int H, int L, int D,
                          int S, float score_scale_log2, int has_c2p, int has_p2c, int dtype,
                          int strict_fp32, void* stream) {
-  // The table contract runs IEEE fp32 MFMA for either precision; the fast
-  // fp32 form (bf16x3) is built for the in-kernel-relative entry points.
-  (void)strict_fp32;
   int rc = check_common(query, key, value, delta_to_local, attention_mask, out, B, H, L, D, S,
                         has_c2p, has_p2c, dtype);
   if (rc == kEmptyBatch) return DFLASH_OK;
@@ -103,7 +100,9 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
   rp.has_p2c = has_p2c;
   rp.splits = 1;
   rp.qw = 32;
-  rp.fast = 0;
+  // fp32 with strict_fp32 = 0: QK and PV on the bf16x3 products (the
+  // reference's TF32 mode, kernel.py:222); the windows are read, not multiplied.
+  rp.fast = (dtype == DFLASH_DTYPE_FP32 && !strict_fp32) ? 1 : 0;
   rp.table = 1;
   return launch_rel_attention(rp, D, dtype, static_cast<hipStream_t>(stream));
 }

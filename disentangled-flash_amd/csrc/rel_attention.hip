@@ -262,7 +262,7 @@ template <typename T, int D, int QW, int BN, int VBUFS, int WGS, bool C2P, bool 
           bool FAST = false, bool TABLE = false, bool ROWSAFE = false>
 __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams p) {
   static_assert(!FAST || sizeof(T) == 4, "the bf16x3 form is for fp32 data");
-  static_assert(!(TABLE && (FAST || SPLIT)), "the table form runs unsplit and in IEEE fp32");
+  static_assert(!(TABLE && SPLIT), "the table form runs unsplit");
   // Relative windows built on the matrix unit from Kr / Qr rows (MC, MP), or
   // read from precomputed c2p / p2c tables (TABLE).
   constexpr bool MC = C2P && !TABLE;
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   QF prow[MP ? PU : 1][KD];    // rows of this wavefront's p2c chunks wave + 4u
   // Fast fp32: prow is kept split; the chunk loaded at the end of a tile waits
   // here (unsplit, its load in flight) until the next tile's p2c products.
-  F prow_in[FAST && P2C ? KD : 1];
+  F prow_in[FAST && MP ? KD : 1];
 
   // ---- table form: the windows read from c2p / p2c tables [B, H, L, S] ----
   //   Cw[q][t]  = c2p[i0w + q][slot(dlo_w + t)],   Pw[jr][t] = p2c[j0 + jr][slot(dlo + t)],
@@ -1022,7 +1022,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
       }
     };
-    if constexpr (FAST && P2C) {
+    if constexpr (FAST && MP) {
       if (j0 != jstart) {
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) prow[0][kd] = to_q(prow_in[kd]);
@@ -1581,12 +1581,13 @@ int rel_modes_qw(const RelParams& prm, hipStream_t stream) {
   if constexpr (sizeof(T) == 4 && !FAST) {
     if (prm.fast) return rel_modes_qw<T, D, QW, true>(prm, stream);
   }
-  // Table form: the default tile of each head dim, 16-bit or IEEE fp32.
-  if constexpr (!FAST && QW == (D >= 128 ? 16 : 32)) {
+  // Table form: the default tile of each head dim, 16-bit or fp32 (IEEE, or
+  // the bf16x3 products of the fast form for QK and PV).
+  if constexpr (QW == (D >= 128 ? 16 : 32)) {
     if (prm.table) {
-      if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true, false, true>(prm, stream);
-      if (prm.has_c2p) return launch_rel<T, D, QW, true, false, false, true>(prm, stream);
-      if (prm.has_p2c) return launch_rel<T, D, QW, false, true, false, true>(prm, stream);
+      if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true, FAST, true>(prm, stream);
+      if (prm.has_c2p) return launch_rel<T, D, QW, true, false, FAST, true>(prm, stream);
+      if (prm.has_p2c) return launch_rel<T, D, QW, false, true, FAST, true>(prm, stream);
     }
   }
   if (prm.has_c2p && prm.has_p2c) return launch_rel<T, D, QW, true, true, FAST>(prm, stream);

@@ -60,9 +60,10 @@ extern "C" {
  *   attention_mask    : uint8 [B, L], nonzero = kept token (the reference's bool mask)
  *   out               : [B, L, H*D], dtype `dtype`
  *   score_scale_log2  : log2(e) / sqrt(D * (1 + has_c2p + has_p2c))  (kernel.py:587-588)
- *   strict_fp32       : accepted for signature parity; this table-reading
- *                       entry point runs IEEE fp32 MFMA for either value (the
- *                       fast fp32 form is built for dflash_attention_rel_fwd).
+ *   strict_fp32       : fp32 only: 1 = IEEE fp32 products; 0 = the reference's
+ *                       TF32 mode (kernel.py:211-223), here QK and PV as three
+ *                       bf16 products each (about 2^-16 relative error per
+ *                       product, against TF32's 2^-11).  Ignored for fp16/bf16.
  * B == 0 is a no-op that returns 0 (pointers are not inspected), like the
  * reference's launch over an empty grid.  query, key, value and out must be
  * 16-byte aligned (DFLASH_ERR_ALIGN); one (b, h) slice of a table,

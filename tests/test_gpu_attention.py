@@ -81,7 +81,7 @@ def _run_rel(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c, key_split
     return out
 
 
-def _run_table(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c):
+def _run_table(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c, strict_fp32=True):
     from disentangled_flash.kernel import deberta_attention
 
     b, h, length, d = q.shape
@@ -91,7 +91,7 @@ def _run_table(q, k, v, pos_key, pos_query, lut, mask, has_c2p, has_p2c):
     out = deberta_attention(q.contiguous(), k.contiguous(), v.contiguous(), c2p, p2c, lut, mask,
                             h, length, pos_key.shape[1], LOG2E / math.sqrt(d * factor),
                             has_c2p, has_p2c, q.dtype == torch.bfloat16, q.dtype == torch.float32,
-                            True)
+                            strict_fp32)
     torch.cuda.synchronize()
     return out
 
@@ -182,6 +182,22 @@ def test_table_kernel_lengths(length, dtype):
     args = _inputs(2, 2, length, 64, DTYPES[dtype], "right", seed=length + 3)
     out = _run_table(*args, True, True)
     _check(out, *args, True, True, f"table L={length}")
+
+
+@pytest.mark.parametrize("dim,heads,length", [(64, 2, 300), (32, 3, 200), (128, 2, 129)])
+@pytest.mark.parametrize("mode", ["both", "c2p", "p2c"])
+def test_table_kernel_fast_fp32(dim, heads, length, mode):
+    """strict_fp32 = False on the reference contract (its TF32 mode): QK and PV as
+    bf16x3 products; held to the fast-fp32 tolerance against the float64 checker,
+    and it must differ from the strict result (the fast path really runs)."""
+
+    has_c2p, has_p2c = MODES[mode]
+    args = _inputs(2, heads, length, dim, torch.float32, "left", seed=dim + length)
+    fast = _run_table(*args, has_c2p, has_p2c, strict_fp32=False)
+    err = _check(fast, *args, has_c2p, has_p2c, f"table fast fp32 d={dim} {mode}", tol=TOL_FAST_FP32)
+    strict = _run_table(*args, has_c2p, has_p2c, strict_fp32=True)
+    print(f"table fast fp32 d={dim} L={length} {mode}: max abs err {err:.2e}", flush=True)
+    assert not torch.equal(fast, strict)
 
 
 @pytest.mark.parametrize("batch,heads,length", [(1, 1, 100), (1, 1, 64), (3, 1, 77), (1, 5, 200)])
