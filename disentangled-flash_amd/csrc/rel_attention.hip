@@ -87,6 +87,38 @@ __device__ inline uint8_t load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
 }
 
+// One buffer_load_dwordx4 with the LDS-direct bit: 16 bytes per lane from
+// `off` to LDS at `lds_base` + 16 * lane (`lds_base` wavefront-uniform, in M0;
+// M0 is restored afterwards).  Out-of-range reads store zeros.  The copy
+// counts in vmcnt like any buffer load, and its LDS writes are awaited with an
+// explicit vmcnt wait (wait_vmem) before the barrier that publishes them.
+// Written as inline assembly so that the compiler does not track the copy:
+// for the builtin it cannot tell the copy's LDS range from that of the
+// transposing V reads and waits for every copy in flight before them.
+__device__ inline void copy16_lds(__amdgpu_buffer_rsrc_t r, uint32_t off, unsigned char* lds_base) {
+  const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_base));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(off), "s"(r)
+      : "memory");
+}
+
+// Wait until at most N of this wavefront's vector-memory operations are pending.
+template <int N>
+__device__ inline void wait_vmem() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Compiler barrier for memory operations: keeps the buffer loads issued after
+// a group of direct copies on their side, so that the vmcnt waits count them.
+__device__ inline void memory_order_point() { asm volatile("" ::: "memory"); }
+
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x8_t __attribute__((ext_vector_type(8)));
@@ -228,17 +260,46 @@ struct IntC {
   static constexpr int value = N;
 };
 
-template <typename T, int D, int QW, int BN, int VBUFS>
+// K and V tiles copied straight from memory into LDS (buffer loads with the
+// LDS-direct bit) instead of through registers: 16-bit data at d >= 64 outside
+// the table form.  A copy instruction writes 64 consecutive 16-byte chunks, so
+// the tiles are unpadded, with the 16-byte chunks of each row permuted by
+// kv_swizzle (below) instead of a row pad.
+template <typename T, int D, bool TABLE>
+constexpr bool rel_kv_direct() {
+  return sizeof(T) == 2 && D >= 64 && !TABLE;
+}
+
+// Chunk permutation of row `row` of a directly copied K / V tile: logical
+// 16-byte chunk x of the row sits at chunk x ^ kv_swizzle(row).  With
+// row = 4a + b (bits 0-3):
+//   * K fragment reads (16 bytes, rows key_of(c) of a 16-key block, one chunk
+//     per lane group g): the eight rows of lanes c = 0..7 (or 8..15) land in
+//     eight different chunks of a 128-byte bank window, and, at d = 64, the
+//     sixteen rows of a 16-lane group in sixteen different 16-byte slots of a
+//     256-byte window;
+//   * V transposing reads (8 bytes, rows 4a + g, 32-byte pairs of chunks,
+//     pair index x >> 1 ^ kv_swizzle >> 1): the four rows of a 16-lane group
+//     land in four different pairs of a 128-byte window.
+template <int D>
+__device__ constexpr int kv_swizzle(int row) {
+  const int a = (row >> 2) & 3;
+  const int b0 = row & 1;
+  const int b1 = (row >> 1) & 1;
+  return D == 64 ? ((b0 ^ b1) | (a << 1)) : (b0 | (a << 1) | (b1 << 3));
+}
+
+template <typename T, int D, int QW, int BN, int VBUFS, bool KV_DIRECT = false>
 struct RelLayout {
   static constexpr int BM = kWaves * QW;                // query rows per workgroup
   static constexpr int NCC = (QW + BN - 1 + 15) / 16;   // c2p window chunks per wavefront
   static constexpr int NPC = (BM + BN - 1 + 15) / 16;   // p2c window chunks per workgroup
   static constexpr int PU = (NPC + kWaves - 1) / kWaves;  // p2c chunks per wavefront
-  static constexpr int KS_LD = D + 8;                   // Ks[BN][KS_LD]
+  static constexpr int KS_LD = KV_DIRECT ? D : D + 8;   // Ks[BN][KS_LD]
   // V tile row-major, Vs[BN][VS_LD]: the row pad of 4 elements makes the
   // transposing reads of the PV operand conflict-free (two passes per
   // half-wavefront) with the staging stores at their minimum.
-  static constexpr int VS_LD = D + 4;
+  static constexpr int VS_LD = KV_DIRECT ? D : D + 4;
   // Row strides (in elements) chosen for the LDS of gfx950 as measured: 32
   // four-byte banks served per half-wavefront, a 2-byte read of two lanes in
   // one dword is a broadcast.  With them the score gathers (lanes = 16 queries
@@ -279,7 +340,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
-  using LY = RelLayout<T, D, QW, BN, VBUFS>;
+  constexpr bool kDirect = rel_kv_direct<T, D, TABLE>();
+  using LY = RelLayout<T, D, QW, BN, VBUFS, kDirect>;
   constexpr int BM = LY::BM;
   constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
   constexpr int KB = BN / 16;           // 16-key blocks per tile
@@ -296,6 +358,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   static_assert(BN % 32 == 0 && BN <= 64, "key tile must be 32 or 64 keys");
   static_assert(QW % 16 == 0, "query rows per wavefront must be a multiple of 16");
   static_assert(NKC % kThreads == 0 || NKC < kThreads, "K tile must split evenly over the workgroup");
+  static_assert(!kDirect || NKC % kThreads == 0, "direct copies: whole rounds of 64 chunks per wavefront");
 
   extern __shared__ __align__(16) unsigned char smem[];
   T* Ks = reinterpret_cast<T*>(smem + LY::ks_off);
@@ -402,7 +465,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     const int t = tid + n * kThreads;
     const int r = t / CPR;
     const int cc = t - r * CPR;
-    koff[n] = static_cast<uint32_t>(r) * sl_bytes + cc * 16;
+    // Direct copies: LDS chunk t holds logical chunk cc ^ kv_swizzle(r) of row r.
+    const int src = kDirect ? (cc ^ kv_swizzle<D>(r)) : cc;
+    koff[n] = static_cast<uint32_t>(r) * sl_bytes + src * 16;
     kls[n] = static_cast<uint32_t>(r * LY::KS_LD + cc * E16);
   }
   // V chunks: the same rows and 16-byte chunks as K.
@@ -614,6 +679,19 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       if (NKC >= kThreads || tid < NKC) dv[n] = load16(rv, koff[n] + jb);
   };
   auto prefetch_k = [&](int j0) { prefetch_k_into(j0, pk, pmask); };
+  // Direct copies of the K / V tile at key offset j0 into LDS (kDirect).
+  auto copy_k = [&](int j0) {
+    const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
+#pragma unroll
+    for (int n = 0; n < NCH; ++n)
+      copy16_lds(rk, koff[n] + jb, smem + LY::ks_off + (n * kThreads + wave * 64) * 16);
+  };
+  auto copy_v = [&](int j0, T* vs) {
+    const uint32_t jb = static_cast<uint32_t>(j0) * sl_bytes;
+#pragma unroll
+    for (int n = 0; n < NVB; ++n)
+      copy16_lds(rv, koff[n] + jb, reinterpret_cast<unsigned char*>(vs) + (n * kThreads + wave * 64) * 16);
+  };
   auto prefetch_v = [&](int j0) { prefetch_v_into(j0, pv); };
 
   // ---- staging and window helpers ----
@@ -654,6 +732,16 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
         }
       }
+  };
+  // Element offset in Ks of the 16-bit K fragment of key row `row` (a row
+  // key_of(c) of a 16-key block), k-step kd: chunk 4 kd + g of the row.
+  const int k_swz = kv_swizzle<D>(key_of(c));
+  auto k_elem = [&](int row, int kd) -> int {
+    if constexpr (kDirect) {
+      return row * D + 8 * ((4 * kd + g) ^ k_swz);
+    } else {
+      return row * LY::KS_LD + 32 * kd + 8 * g;
+    }
   };
   // Fast fp32: K fragment of key row `row`, k-step kd, from the split planes.
   auto k_read = [&](int row, int kd) -> QF {
@@ -844,8 +932,18 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     for (int kd = 0; kd < KD; ++kd)
       qf[qb][kd] = to_q(load_frag<T>(rq, static_cast<uint32_t>(i) * sl_bytes + (32 * kd + 8 * g) * ES));
   }
-  prefetch_k(jstart);
-  prefetch_v(jstart);
+  if constexpr (kDirect) {
+    // Mask bytes first: the copies are waited for by counting the buffer
+    // loads issued after them (kLoadsAfterCopies).
+    pmask = load1(rmask, static_cast<uint32_t>(jstart + lane));
+    memory_order_point();
+    copy_k(jstart);
+    if constexpr (VBUFS == 2) copy_v(jstart, Vt);
+    memory_order_point();
+  } else {
+    prefetch_k(jstart);
+    prefetch_v(jstart);
+  }
   // Tile 1 (d = 64 only: d = 128 has no registers to spare here, and d = 32,
   // whose tiles are short, measured faster without it): K/V and the rows of
   // its new c2p chunks (lookups in lutc), moved into the pipeline registers
@@ -855,7 +953,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   u32x4_t pv1[NVB];
   uint8_t pmask1 = 0;
   F crow1[MC && kEarlyTile1 ? kSlide : 1][KD];
-  if constexpr (kEarlyTile1) {
+  if constexpr (kEarlyTile1 && kDirect) {
+    pmask1 = load1(rmask, static_cast<uint32_t>(jstart + BN + lane));
+  } else if constexpr (kEarlyTile1) {
     prefetch_k_into(jstart + BN, pk1, pmask1);
     if constexpr (VBUFS == 2) prefetch_v_into(jstart + BN, pv1);
   }
@@ -898,17 +998,21 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         for (int r = 0; r < 4; ++r) ccar[ch][qb][r] = static_cast<T>(acc[r]);
       }
   }
-  stage_k();
-  if constexpr (VBUFS == 2) stage_v(Vt);
+  if constexpr (!kDirect) {
+    stage_k();
+    if constexpr (VBUFS == 2) stage_v(Vt);
+  }
   uint64_t kept_cur = __ballot(pmask != 0);  // keys j0 + lane (zero past L)
   uint64_t kept_next = 0;
   c2p_products();
   c2p_store();
   if constexpr (kEarlyTile1) {
+    if constexpr (!kDirect) {
 #pragma unroll
-    for (int n = 0; n < NCH; ++n) pk[n] = pk1[n];
+      for (int n = 0; n < NCH; ++n) pk[n] = pk1[n];
+    }
     pmask = pmask1;
-    if constexpr (VBUFS == 2) {
+    if constexpr (VBUFS == 2 && !kDirect) {
 #pragma unroll
       for (int n = 0; n < NVB; ++n) pv[n] = pv1[n];
     }
@@ -920,11 +1024,24 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         lutc[ch] = lut_load(lut_c_index(jstart + 2 * BN, ch));
       }
     }
+  } else if constexpr (kDirect) {
+    pmask = load1(rmask, static_cast<uint32_t>(jstart + BN + lane));
+    load_crow(jstart + BN);
   } else {
     prefetch_k(jstart + BN);
     if constexpr (VBUFS == 2) prefetch_v(jstart + BN);
     load_crow(jstart + BN);
   }
+  // Direct copies: buffer loads a wavefront issues after the K / V copies of
+  // a tile and before the wait for them (at the top of the next tile): the
+  // mask byte is issued before the copies, then come the c2p rows and
+  // lookups of load_crow.  The prologue issues at least as many after its
+  // copies.  With one V buffer, V is copied after the first barrier of its
+  // tile and waited for before the second; the p2c rows and lookup are
+  // issued in between.
+  constexpr int kLoadsAfterCopies = MC ? kSlide * (KD + 1) : 0;
+  constexpr int kLoadsAfterV = MP ? KD + 1 : 0;
+  static_assert(!kDirect || sizeof(T) == 2, "one buffer load per row fragment");
 
   // ---- accumulators ----
   f32x4_t o[DB][kQB];
@@ -950,6 +1067,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   const T* pw_lane = Pw + g * LY::PW_LD + QW * wave + c - g + BN - 1 + kMinOff;
   const float scale = p.scale_log2;
   const F ones = ones_frag<T>();
+  const int v_swz = kv_swizzle<D>(4 * (c >> 2) + g);
 
   // Per tile: barrier B (K/V staged, previous gathers done) -> QK, p2c window;
   // barrier C (p2c window complete, K tile consumed) -> stage the next K/V,
@@ -957,8 +1075,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   int vbuf = 0;
   for (int j0 = jstart; j0 < jend; j0 += BN) {
     const int jn = j0 + BN;
+    if constexpr (kDirect) wait_vmem<kLoadsAfterCopies>();  // K (and V) of this tile in LDS
     lds_barrier();
-    if constexpr (VBUFS == 1) {
+    if constexpr (VBUFS == 1 && kDirect) {
+      memory_order_point();
+      copy_v(j0, Vt);
+      memory_order_point();
+    } else if constexpr (VBUFS == 1) {
       stage_v(Vt);
       prefetch_v(SPLIT && jn >= jend ? L : jn);
     }
@@ -982,7 +1105,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         if constexpr (FAST) {
           kfa[0][kd] = k_read(key_of(c), kd);
         } else {
-          kfa[0][kd] = *reinterpret_cast<const F*>(Ks + key_of(c) * LY::KS_LD + 32 * kd + 8 * g);
+          kfa[0][kd] = *reinterpret_cast<const F*>(Ks + k_elem(key_of(c), kd));
         }
       }
 #pragma unroll
@@ -996,7 +1119,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
             if constexpr (FAST) {
               kfa[(kb + 1) & 1][kd] = k_read(16 * (kb + 1) + key_of(c), kd);
             } else {
-              kfa[(kb + 1) & 1][kd] = *reinterpret_cast<const F*>(Ks + (16 * (kb + 1) + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+              kfa[(kb + 1) & 1][kd] = *reinterpret_cast<const F*>(Ks + k_elem(16 * (kb + 1) + key_of(c), kd));
             }
           }
         }
@@ -1044,7 +1167,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           if constexpr (FAST) {
             kf[kd] = k_read(16 * kb + key_of(c), kd);
           } else {
-            kf[kd] = *reinterpret_cast<const F*>(Ks + (16 * kb + key_of(c)) * LY::KS_LD + 32 * kd + 8 * g);
+            kf[kd] = *reinterpret_cast<const F*>(Ks + k_elem(16 * kb + key_of(c), kd));
           }
         }
 #pragma unroll
@@ -1083,6 +1206,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       }
       lutp = lut_load(lut_p_index(jn + BN, 0));
     }
+    if constexpr (kDirect && VBUFS == 1) wait_vmem<kLoadsAfterV>();  // V of this tile in LDS
     lds_barrier();
 
     // ---- stage the next tile; its c2p products overlap this tile's softmax ----
@@ -1090,14 +1214,24 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     // region): past the last tile the buffer loads read zeros and the LDS
     // writes land in buffers nothing reads any more.
     const T* vt_cur = Vt + (VBUFS == 2 ? vbuf * LY::VT_SIZE : 0);
-    stage_k();
-    if constexpr (VBUFS == 2) stage_v(Vt + (vbuf ^ 1) * LY::VT_SIZE);
-    kept_next = __ballot(pmask != 0);
     // A split's tiles past its range are redirected past L: the buffer loads
     // then return zeros without touching memory.
     const int jpre = SPLIT && jn + BN >= jend ? L : jn + BN;
-    prefetch_k(jpre);
-    if constexpr (VBUFS == 2) prefetch_v(jpre);
+    if constexpr (kDirect) {
+      kept_next = __ballot(pmask != 0);
+      pmask = load1(rmask, static_cast<uint32_t>(jpre + lane));
+      memory_order_point();
+      const int jcopy = SPLIT && jn >= jend ? L : jn;
+      copy_k(jcopy);
+      if constexpr (VBUFS == 2) copy_v(jcopy, Vt + (vbuf ^ 1) * LY::VT_SIZE);
+      memory_order_point();
+    } else {
+      stage_k();
+      if constexpr (VBUFS == 2) stage_v(Vt + (vbuf ^ 1) * LY::VT_SIZE);
+      kept_next = __ballot(pmask != 0);
+      prefetch_k(jpre);
+      if constexpr (VBUFS == 2) prefetch_v(jpre);
+    }
     c2p_products();
 
     // ---- relative scores ----
@@ -1182,6 +1316,15 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_hi));
       return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
     };
+    // Element offset in the V tile of lane (c, g)'s 8 bytes of row `row`
+    // (4 (c >> 2) + g of a 16-row group), columns 16 db + 4 (c & 3) .. + 3.
+    auto v_elem = [&](int row, int db) -> int {
+      if constexpr (kDirect) {
+        return row * D + 8 * ((2 * db + ((c & 3) >> 1)) ^ v_swz) + 4 * (c & 1);
+      } else {
+        return row * LY::VS_LD + 16 * db + 4 * (c & 3);
+      }
+    };
     auto vt_frag = [&](int ks, int db) -> QF {
       if constexpr (FAST) {
         // The P^T key order of the 16-bit path is the fp32 one (below), so the
@@ -1204,7 +1347,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         // k-slice][16db + c] -- keys g + 4e and 16 + g + 4e, the order of the P^T
         // operand.  The result is moved as whole dwords: assembling the operand
         // from its 16-bit elements was compiled into wrong code.
-        const T* p_lo = vt_cur + (32 * ks + 4 * (c >> 2) + g) * LY::VS_LD + 16 * db + 4 * (c & 3);
+        const T* p_lo = vt_cur + v_elem(32 * ks + 4 * (c >> 2) + g, db);
         const T* p_hi = p_lo + 16 * LY::VS_LD;
         const u32x2_t lo = __builtin_bit_cast(
             u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)p_lo));
@@ -1327,6 +1470,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     kept_cur = kept_next;
     vbuf ^= 1;
   }
+  // The last tile's copies (of a tile past the end) land before LDS is reused.
+  if constexpr (kDirect) wait_vmem<0>();
 
   // ---- normalise and store [B, L, H*D]; padded rows take the mean of V ----
   float row_sum[kQB];
@@ -1519,7 +1664,7 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
   constexpr int VB = rel_v_buffers<T, D, QW>();
   constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
-  using LY = RelLayout<T, D, QW, BN, VB>;
+  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, TABLE>()>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
