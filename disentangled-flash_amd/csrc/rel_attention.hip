@@ -272,21 +272,25 @@ constexpr bool rel_kv_direct() {
 
 // Chunk permutation of row `row` of a directly copied K / V tile: logical
 // 16-byte chunk x of the row sits at chunk x ^ kv_swizzle(row).  With
-// row = 4a + b (bits 0-3):
-//   * K fragment reads (16 bytes, rows key_of(c) of a 16-key block, one chunk
-//     per lane group g): the eight rows of lanes c = 0..7 (or 8..15) land in
-//     eight different chunks of a 128-byte bank window, and, at d = 64, the
-//     sixteen rows of a 16-lane group in sixteen different 16-byte slots of a
-//     256-byte window;
-//   * V transposing reads (8 bytes, rows 4a + g, 32-byte pairs of chunks,
-//     pair index x >> 1 ^ kv_swizzle >> 1): the four rows of a 16-lane group
-//     land in four different pairs of a 128-byte window.
+// row = 4a + b (bits 0-3), b = 2 b1 + b0:
+//   * K fragment reads (16 bytes per lane, rows key_of(c) of a 16-key block,
+//     one chunk per lane group g): the eight rows of lanes c = 0..7 (or
+//     8..15), b1 fixed, land in eight different chunks of a 128-byte bank
+//     window (a and b0 are in bits 0-2);
+//   * V transposing reads (8 bytes per lane, rows 4a + g, four lanes per
+//     32-byte pair of chunks, pair x >> 1 ^ kv_swizzle >> 1): the rows served
+//     together - four (a) per 16 lanes, eight (a, b0) per 32 lanes - land in
+//     different pairs (a in bits 1-2, b0 in bit 3 at d = 128; at d = 64 a row
+//     is 128 bytes, so rows of different b0 already sit in different halves of
+//     a 256-byte window).
+// Measured at d = 128 (C5): 56 bank-conflict units per wavefront, against
+// 297 with b1 in bit 3 (conflict-free for 16-lane groups only).
 template <int D>
 __device__ constexpr int kv_swizzle(int row) {
   const int a = (row >> 2) & 3;
   const int b0 = row & 1;
   const int b1 = (row >> 1) & 1;
-  return D == 64 ? ((b0 ^ b1) | (a << 1)) : (b0 | (a << 1) | (b1 << 3));
+  return D == 64 ? ((b0 ^ b1) | (a << 1)) : (b0 | (a << 1) | (b0 << 3));
 }
 
 template <typename T, int D, int QW, int BN, int VBUFS, bool KV_DIRECT = false>
