@@ -261,13 +261,14 @@ struct IntC {
 };
 
 // K and V tiles copied straight from memory into LDS (buffer loads with the
-// LDS-direct bit) instead of through registers: 16-bit data at d >= 64 outside
-// the table form.  A copy instruction writes 64 consecutive 16-byte chunks, so
+// LDS-direct bit) instead of through registers: 16-bit data at d >= 64, in the
+// table form with two V buffers only (with one, the wait for the V copy would
+// also wait for the table loads issued after it).  A copy instruction writes 64 consecutive 16-byte chunks, so
 // the tiles are unpadded, with the 16-byte chunks of each row permuted by
 // kv_swizzle (below) instead of a row pad.
-template <typename T, int D, bool TABLE>
+template <typename T, int D, int VBUFS, bool TABLE>
 constexpr bool rel_kv_direct() {
-  return sizeof(T) == 2 && D >= 64 && !TABLE;
+  return sizeof(T) == 2 && D >= 64 && (!TABLE || VBUFS == 2);
 }
 
 // Chunk permutation of row `row` of a directly copied K / V tile: logical
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
-  constexpr bool kDirect = rel_kv_direct<T, D, TABLE>();
+  constexpr bool kDirect = rel_kv_direct<T, D, VBUFS, TABLE>();
   using LY = RelLayout<T, D, QW, BN, VBUFS, kDirect>;
   constexpr int BM = LY::BM;
   constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
@@ -537,9 +538,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // e = lane + 64k of the wavefront's QW x NCW c2p window is (q, t) =
   // (e / NCW, e % NCW): t repeats with period TC_P in k while q advances by TC_R
   // per period, so a lane needs TC_P lookups per tile.  The p2c window (BN x NPW)
-  // is split the same way over the workgroup's threads (e = tid + 256k).  Loads
-  // of tile n+1 are issued after the gathers of tile n and stored after barrier
-  // B of tile n+1 (every wavefront is past its gathers of tile n then).
+  // is split the same way over the workgroup's threads (e = tid + 256k).  The
+  // values of tile n+1 are stored after barrier B of tile n+1 (every wavefront
+  // is past its gathers of tile n then).  Its p2c values are loaded a whole tile
+  // ahead, right after barrier B of tile n (lookups two tiles ahead); its c2p
+  // values after the gathers of tile n (both early spill registers: 296 against
+  // 153 us at C2).  `sel` picks the windows: bit 0 c2p, bit 1 p2c.
   constexpr int NCW = NCC * 16;
   constexpr int NPW = NPC * 16;
   constexpr bool TC = TABLE && C2P;
@@ -605,14 +609,14 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // reference), but its offset stays inside its table row, so that with the
   // row step in soffset (unchecked) no read leaves the tensor.
   const uint32_t slot_max = static_cast<uint32_t>(p.S - 1);
-  auto table_lookups = [&](int j0) {
-    if constexpr (TC) {
+  auto table_lookups = [&](int j0, auto sel) {
+    if constexpr (TC && (decltype(sel)::value & 1)) {
 #pragma unroll
       for (int pp = 0; pp < TC_P; ++pp)
         tc_slot[pp] = static_cast<int>(
             min(static_cast<uint32_t>(lut_load(i0w - j0 - (BN - 1) + tc_t[pp] + L - 1)), slot_max));
     }
-    if constexpr (TP) {
+    if constexpr (TP && (decltype(sel)::value & 2)) {
 #pragma unroll
       for (int pp = 0; pp < TP_P; ++pp)
         tp_slot[pp] = static_cast<int>(
@@ -621,8 +625,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   };
   // Window values of the tile at key offset j0 (slots from table_lookups(j0)).
   // Rows past L read as zero through the buffer bounds.
-  auto table_load = [&](int j0) {
-    if constexpr (TC) {
+  auto table_load = [&](int j0, auto sel) {
+    if constexpr (TC && (decltype(sel)::value & 1)) {
 #pragma unroll
       for (int pp = 0; pp < TC_P; ++pp) {
         const uint32_t voff = static_cast<uint32_t>(tc_slot[pp]) * ES +
@@ -632,7 +636,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           tcv[pp + TC_P * m] = row_load(rtc, voff, static_cast<uint32_t>(m * TC_R) * row_bytes);
       }
     }
-    if constexpr (TP) {
+    if constexpr (TP && (decltype(sel)::value & 2)) {
 #pragma unroll
       for (int pp = 0; pp < TP_P; ++pp) {
         const uint32_t voff = static_cast<uint32_t>(tp_slot[pp]) * ES +
@@ -853,7 +857,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   // ---- prologue: loads of tile 0, in the order their results are needed ----
   // Lookups first (they depend only on the block).
-  table_lookups(jstart);
+  table_lookups(jstart, IntC<3>{});
   int lc[MC ? NCC : 1];
   int lp[MP ? PU : 1];
   if constexpr (MC) {
@@ -911,7 +915,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
   // Rows of the tile-0 windows, then Q and the K/V of tile 0 (a workgroup
   // without kept queries has left before issuing them).
-  table_load(jstart);
+  table_load(jstart, IntC<3>{});
+  table_lookups(jstart + BN, IntC<2>{});
   F r0[MC && kCarry > 0 ? kCarry : 1][KD];
   if constexpr (MC) {
 #pragma unroll
@@ -1040,7 +1045,8 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // a tile and before the wait for them (at the top of the next tile): the
   // mask byte is issued before the copies, then come the c2p rows and
   // lookups of load_crow.  The prologue issues at least as many after its
-  // copies.  With one V buffer, V is copied after the first barrier of its
+  // copies.  (The table form waits for everything: its c2p table loads, issued
+  // after the copies, are stored right after that barrier anyway.)  With one V buffer, V is copied after the first barrier of its
   // tile and waited for before the second; the p2c rows and lookup are
   // issued in between.
   constexpr int kLoadsAfterCopies = MC ? kSlide * (KD + 1) : 0;
@@ -1089,9 +1095,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       stage_v(Vt);
       prefetch_v(SPLIT && jn >= jend ? L : jn);
     }
-    // Table form: windows of this tile into LDS, lookups of the next.
+    // Table form: windows of this tile into LDS; p2c values of the next tile,
+    // p2c lookups of the one after, c2p lookups of the next.
     table_store();
-    table_lookups(jn);
+    table_load(jn, IntC<2>{});
+    table_lookups(jn + BN, IntC<2>{});
+    table_lookups(jn, IntC<1>{});
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
     f32x4_t sc[KB][kQB];
@@ -1278,7 +1287,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       }
     }
 
-    table_load(jn);
+    table_load(jn, IntC<1>{});
 
     // ---- masking (wavefront-uniform slow path: tiles with a padded key or past L) ----
     // Every row drops the padded keys.  That is the rule for kept queries; the
@@ -1668,7 +1677,7 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
   constexpr int VB = rel_v_buffers<T, D, QW>();
   constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
-  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, TABLE>()>;
+  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE>()>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
