@@ -31,8 +31,12 @@
 // tile through LDS and writes it in coalesced 16-byte chunks.
 //
 // Launch order: workgroup p runs on XCD p % 8.  Each XCD takes a contiguous
-// range of row blocks and walks its column blocks fastest, so the tiles of
-// one X row block run on the same XCD at the same time and share its L2.
+// range of tiles.  When X is the larger operand (M >= N: many rows) the range
+// is row-major (column blocks fastest), so the tiles of one X row block run on
+// the same XCD and share its L2, and every XCD streams all of W; when W is the
+// larger (few rows) it is column-major, so every XCD streams all of X and only
+// its own slice of W (at 512 rows this takes the 1536-wide QKV from 26.2 to
+// 17.9 us and the FFN intermediate from 28.0 to 21.6 us, bf16).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -167,6 +171,7 @@ struct GemmArgs {
   void* y;
   int M, N, K;
   int m_blocks, n_blocks;
+  int col_major;  // tile order within an XCD's range: column blocks slowest
 };
 
 template <typename T, int EPI, typename CF>
@@ -194,8 +199,14 @@ __global__ __launch_bounds__(CF::THREADS, CF::WGS) void gemm_kernel(GemmArgs a) 
   const int per_xcd = (total + 7) >> 3;
   const int t = (p & 7) * per_xcd + (p >> 3);
   if (t >= total) return;  // padding of the grid to a multiple of 8
-  const int mb = t / a.n_blocks;
-  const int nb = t - mb * a.n_blocks;
+  int mb, nb;
+  if (a.col_major) {
+    nb = t / a.m_blocks;
+    mb = t - nb * a.m_blocks;
+  } else {
+    mb = t / a.n_blocks;
+    nb = t - mb * a.n_blocks;
+  }
   const int m_base = mb * CF::BM;
   const int n_base = nb * BN;
   const int K = a.K;
@@ -402,6 +413,11 @@ int launch_gemm(GemmArgs args, hipStream_t stream) {
   if (err != hipSuccess) return static_cast<int>(err);
   args.m_blocks = (args.M + CF::BM - 1) / CF::BM;
   args.n_blocks = args.N / CF::BN;
+  // Each XCD walks a contiguous range of tiles.  Row-major ranges make every
+  // XCD read the whole of W (and its own rows of X), column-major ones the
+  // whole of X (and its own slice of W): take the order whose repeated operand
+  // is the smaller.
+  args.col_major = args.N > args.M ? 1 : 0;
   const int64_t tiles = static_cast<int64_t>(args.m_blocks) * args.n_blocks;
   const int64_t grid = ((tiles + 7) / 8) * 8;
   if (grid > 0x7fffffff) return DFLASH_ERR_TOO_LARGE;
