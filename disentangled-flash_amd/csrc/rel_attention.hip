@@ -263,9 +263,9 @@ struct IntC {
 // K and V tiles copied straight from memory into LDS (buffer loads with the
 // LDS-direct bit) instead of through registers: 16-bit data at d >= 64, in the
 // table form with two V buffers only (with one, the wait for the V copy would
-// also wait for the table loads issued after it).  A copy instruction writes 64 consecutive 16-byte chunks, so
-// the tiles are unpadded, with the 16-byte chunks of each row permuted by
-// kv_swizzle (below) instead of a row pad.
+// also wait for the table loads issued after it).  A copy instruction writes
+// 64 consecutive 16-byte chunks, so the tiles are unpadded, with the 16-byte
+// chunks of each row permuted by kv_swizzle (below) instead of a row pad.
 template <typename T, int D, int VBUFS, bool TABLE>
 constexpr bool rel_kv_direct() {
   return sizeof(T) == 2 && D >= 64 && (!TABLE || VBUFS == 2);
