@@ -261,14 +261,17 @@ struct IntC {
 };
 
 // K and V tiles copied straight from memory into LDS (buffer loads with the
-// LDS-direct bit) instead of through registers: 16-bit data at d >= 64, in the
-// table form with two V buffers only (with one, the wait for the V copy would
-// also wait for the table loads issued after it).  A copy instruction writes
-// 64 consecutive 16-byte chunks, so the tiles are unpadded, with the 16-byte
+// LDS-direct bit) instead of through registers: 16-bit data at d >= 64.  With
+// one V buffer, V is copied after the first barrier of its tile and awaited at
+// the second, so the QK phase in between must hide the copy: not in the table
+// form (the wait would also wait for the table loads issued after the copy),
+// and only with the p2c products in that phase (without them, C5 d = 128 c2p
+// ran 79.7 against 76.9 us through registers).  A copy instruction writes 64
+// consecutive 16-byte chunks, so the tiles are unpadded, with the 16-byte
 // chunks of each row permuted by kv_swizzle (below) instead of a row pad.
-template <typename T, int D, int VBUFS, bool TABLE>
+template <typename T, int D, int VBUFS, bool TABLE, bool P2C>
 constexpr bool rel_kv_direct() {
-  return sizeof(T) == 2 && D >= 64 && (!TABLE || VBUFS == 2);
+  return sizeof(T) == 2 && D >= 64 && (VBUFS == 2 || (!TABLE && P2C));
 }
 
 // Chunk permutation of row `row` of a directly copied K / V tile: logical
@@ -345,7 +348,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     }
   };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
-  constexpr bool kDirect = rel_kv_direct<T, D, VBUFS, TABLE>();
+  constexpr bool kDirect = rel_kv_direct<T, D, VBUFS, TABLE, P2C>();
   using LY = RelLayout<T, D, QW, BN, VBUFS, kDirect>;
   constexpr int BM = LY::BM;
   constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
@@ -1677,7 +1680,7 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
   constexpr int VB = rel_v_buffers<T, D, QW>();
   constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
-  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE>()>;
+  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE, P2C>()>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
