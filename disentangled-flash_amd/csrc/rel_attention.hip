@@ -180,6 +180,47 @@ struct RelMmaFast {
   }
 };
 
+// Strict fp32 products on the bf16 matrix unit (bf16x6): each fp32 value is
+// split into x = hi + mid + lo, three bf16 parts holding its 24 significand
+// bits (hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid)), and a.b
+// keeps the six part products down to 2^-16 of the leading one: lo.hi, hi.lo,
+// mid.mid, mid.hi, hi.mid, hi.hi (smallest first).  The dropped mid.lo,
+// lo.mid and lo.lo are below 2^-24 of it, fp32's own rounding; accumulation is
+// fp32.  Six v_mfma_f32_16x16x32_bf16 (96 cycles) replace eight
+// v_mfma_f32_16x16x4f32 (256 cycles) per 32-deep product.
+struct RelMmaExact {
+  using frag = f32x8_t;
+  struct split_frag {
+    bf16x8_t hi, mid, lo;
+  };
+  __device__ static split_frag split(const f32x8_t& x) {
+    split_frag s;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const __bf16 h = static_cast<__bf16>(x[e]);
+      const float r = x[e] - static_cast<float>(h);
+      const __bf16 m = static_cast<__bf16>(r);
+      s.hi[e] = h;
+      s.mid[e] = m;
+      s.lo[e] = static_cast<__bf16>(r - static_cast<float>(m));
+    }
+    return s;
+  }
+  __device__ static const split_frag& as_split(const split_frag& x) { return x; }
+  __device__ static split_frag as_split(const f32x8_t& x) { return split(x); }
+  template <typename A, typename B>
+  __device__ static f32x4_t run(const A& a, const B& b, f32x4_t c) {
+    const split_frag sa = as_split(a);
+    const split_frag sb = as_split(b);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.lo, sb.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.hi, sb.lo, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.mid, sb.mid, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.mid, sb.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.hi, sb.mid, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(sa.hi, sb.hi, c, 0, 0, 0);
+  }
+};
+
 // Elements of T per 16-byte chunk.
 template <typename T>
 constexpr int kChunkElems = 16 / static_cast<int>(sizeof(T));
@@ -336,13 +377,17 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   // read from precomputed c2p / p2c tables (TABLE).
   constexpr bool MC = C2P && !TABLE;
   constexpr bool MP = P2C && !TABLE;
-  using M = std::conditional_t<FAST, RelMmaFast, RelMma<T>>;
+  // fp32 on the bf16 matrix unit: bf16x3 (FAST) or bf16x6 (strict, EXACT).
+  constexpr bool EXACT = sizeof(T) == 4 && !FAST && D <= 64;
+  constexpr bool SPLITQ = FAST || EXACT;
+  using M = std::conditional_t<FAST, RelMmaFast, std::conditional_t<EXACT, RelMmaExact, RelMma<T>>>;
   using F = typename M::frag;
-  // Fragments that feed several products: split once in the fast fp32 form.
-  using QF = std::conditional_t<FAST, typename RelMmaFast::split_frag, F>;
+  // Fragments that feed several products: split once in the fp32 forms.
+  using QF = std::conditional_t<FAST, typename RelMmaFast::split_frag,
+                                std::conditional_t<EXACT, typename RelMmaExact::split_frag, F>>;
   auto to_q = [](const F& x) -> QF {
-    if constexpr (FAST) {
-      return RelMmaFast::split(x);
+    if constexpr (SPLITQ) {
+      return M::split(x);
     } else {
       return x;
     }
@@ -531,7 +576,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   QF prow[MP ? PU : 1][KD];    // rows of this wavefront's p2c chunks wave + 4u
   // Fast fp32: prow is kept split; the chunk loaded at the end of a tile waits
   // here (unsplit, its load in flight) until the next tile's p2c products.
-  F prow_in[FAST && MP ? KD : 1];
+  F prow_in[SPLITQ && MP ? KD : 1];
 
   // ---- table form: the windows read from c2p / p2c tables [B, H, L, S] ----
   //   Cw[q][t]  = c2p[i0w + q][slot(dlo_w + t)],   Pw[jr][t] = p2c[j0 + jr][slot(dlo + t)],
@@ -790,7 +835,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   Quad<T> cnew[MC ? kSlide : 1][kQB];
   auto c2p_products = [&]() {
     if constexpr (MC) {
-      if constexpr (FAST) {
+      if constexpr (SPLITQ) {
         // Each row fragment split once for its kQB products.
 #pragma unroll
         for (int ch = 0; ch < kSlide; ++ch) {
@@ -1121,7 +1166,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         if constexpr (FAST) {
           kfa[0][kd] = k_read(key_of(c), kd);
         } else {
-          kfa[0][kd] = *reinterpret_cast<const F*>(Ks + k_elem(key_of(c), kd));
+          kfa[0][kd] = to_q(*reinterpret_cast<const F*>(Ks + k_elem(key_of(c), kd)));
         }
       }
 #pragma unroll
@@ -1135,7 +1180,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
             if constexpr (FAST) {
               kfa[(kb + 1) & 1][kd] = k_read(16 * (kb + 1) + key_of(c), kd);
             } else {
-              kfa[(kb + 1) & 1][kd] = *reinterpret_cast<const F*>(Ks + k_elem(16 * (kb + 1) + key_of(c), kd));
+              kfa[(kb + 1) & 1][kd] = to_q(*reinterpret_cast<const F*>(Ks + k_elem(16 * (kb + 1) + key_of(c), kd)));
             }
           }
         }
@@ -1161,7 +1206,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         }
       }
     };
-    if constexpr (FAST && MP) {
+    if constexpr (SPLITQ && MP) {
       if (j0 != jstart) {
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) prow[0][kd] = to_q(prow_in[kd]);
@@ -1183,7 +1228,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           if constexpr (FAST) {
             kf[kd] = k_read(16 * kb + key_of(c), kd);
           } else {
-            kf[kd] = *reinterpret_cast<const F*>(Ks + k_elem(16 * kb + key_of(c), kd));
+            kf[kd] = to_q(*reinterpret_cast<const F*>(Ks + k_elem(16 * kb + key_of(c), kd)));
           }
         }
 #pragma unroll
@@ -1214,7 +1259,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         for (int kd = 0; kd < KD; ++kd) prow[u][kd] = prow[u - 1][kd];
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
-        if constexpr (FAST) {
+        if constexpr (SPLITQ) {
           prow_in[kd] = row_frag(rqr, lutp, kd);
         } else {
           prow[0][kd] = row_frag(rqr, lutp, kd);
@@ -1356,7 +1401,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           a[e] = col[(32 * ks + (e < 4 ? 0 : 16) + g + 4 * (e & 3)) * LY::VS_LD];
-        return a;
+        return to_q(a);
       } else {
         // Lane c of group g supplies row 32ks + 4(c>>2) + g (+16 for the upper
         // half), columns 16db + 4(c&3) .. +3, and receives V[rows of its
@@ -1372,7 +1417,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         return __builtin_bit_cast(F, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
       }
     };
-    constexpr bool kVtEarly = D >= 128 && !SPLIT && !TABLE && C2P && P2C;
+    constexpr bool kVtEarly = D >= 128 && !SPLIT && !TABLE && C2P && P2C && !EXACT;
     QF vt_all[kVtEarly ? BN / 32 : 1][kVtEarly ? DB : 1];
     if constexpr (kVtEarly) {
 #pragma unroll
@@ -1449,8 +1494,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           rs[qb] = M::run(ones, pf[qb], rs[qb]);
         }
       }
-      if constexpr (FAST) {
-        // P split once for its DB products; V^T comes split from the planes.
+      if constexpr (SPLITQ) {
+        // P split once for its DB products; V^T comes split (from the planes,
+        // or split where it is read).
         QF pq[kQB];
 #pragma unroll
         for (int qb = 0; qb < kQB; ++qb) pq[qb] = to_q(pf[qb]);

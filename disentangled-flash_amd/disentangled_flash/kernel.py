@@ -342,11 +342,13 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
     """Forward-only MI355X DeBERTa-v2/v3 self-attention.
 
     Head dimensions 32, 64 and 128; fp16, bf16 and fp32.  ``fp32_precision``
-    follows the reference (``kernel.py:485-493``): ``"strict"`` runs IEEE fp32
-    MFMA; ``"fast"`` is TF32 there, and gfx950 has no TF32 matrix path, so the
-    fused kernel splits each fp32 operand into bf16 hi + lo and runs every
-    product as three bf16 MFMAs (relative error about 2^-16 per product, below
-    TF32's 2^-11).  ``relative_mode="table"`` runs IEEE fp32 in either mode.
+    follows the reference (``kernel.py:485-493``): ``"strict"`` gives fp32-accurate
+    products (IEEE fp32 MFMA at d = 128; at d <= 64 six bf16 MFMAs over a
+    three-way bf16 split of each operand, which keeps all 24 significand bits);
+    ``"fast"`` is TF32 there, and gfx950 has no TF32 matrix path, so the fused
+    kernel splits each fp32 operand into bf16 hi + lo and runs every product as
+    three bf16 MFMAs (relative error about 2^-16 per product, below TF32's
+    2^-11).  ``relative_mode="table"`` follows the same two modes for QK and PV.
 
     ``relative_mode="fused"`` (default) computes the c2p/p2c scores inside the
     attention kernel; ``"table"`` reproduces the reference's data flow (two

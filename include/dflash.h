@@ -60,7 +60,8 @@ extern "C" {
  *   attention_mask    : uint8 [B, L], nonzero = kept token (the reference's bool mask)
  *   out               : [B, L, H*D], dtype `dtype`
  *   score_scale_log2  : log2(e) / sqrt(D * (1 + has_c2p + has_p2c))  (kernel.py:587-588)
- *   strict_fp32       : fp32 only: 1 = IEEE fp32 products; 0 = the reference's
+ *   strict_fp32       : fp32 only: 1 = fp32-accurate products (as for the
+ *                       relative entry points below); 0 = the reference's
  *                       TF32 mode (kernel.py:211-223), here QK and PV as three
  *                       bf16 products each (about 2^-16 relative error per
  *                       product, against TF32's 2^-11).  Ignored for fp16/bf16.
@@ -94,9 +95,13 @@ DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const vo
  *                       (kernel.py:461-468, 522-523)
  *   delta_to_local    : as above; any table (the kernel builds its relative
  *                       windows per delta, gathering rows through the table).
- *   strict_fp32       : fp32 only.  1 = IEEE fp32 MFMA (v_mfma_f32_16x16x4_f32),
- *                       the reference's strict mode (input_precision="ieee",
- *                       kernel.py:216).  0 = the reference's fast mode, which is
+ *   strict_fp32       : fp32 only.  1 = the reference's strict mode
+ *                       (input_precision="ieee", kernel.py:216): fp32-accurate
+ *                       products, IEEE fp32 MFMA (v_mfma_f32_16x16x4_f32) at
+ *                       D = 128 and, at D <= 64, six bf16 MFMAs over a
+ *                       three-way bf16 split of each operand (all 24 significand
+ *                       bits; the dropped part products are below 2^-24 of the
+ *                       leading one).  0 = the reference's fast mode, which is
  *                       TF32 there (kernel.py:222); gfx950 has no TF32 matrix
  *                       path, so each fp32 operand is split into bf16 hi + lo
  *                       and the product runs as three bf16 MFMAs (relative error
