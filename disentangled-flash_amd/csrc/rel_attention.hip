@@ -338,7 +338,15 @@ __device__ constexpr int kv_swizzle(int row) {
   return D == 64 ? ((b0 ^ b1) | (a << 1)) : (b0 | (a << 1) | (b0 << 3));
 }
 
-template <typename T, int D, int QW, int BN, int VBUFS, bool KV_DIRECT = false>
+// Strict fp32 at d = 32 stages K and V already split into three bf16 planes
+// (hi, mid, lo: 6 bytes per element, 1.5 times the fp32 tile), which fits the
+// LDS at this head size only (d = 64 fills it with the fp32 tiles).
+template <typename T, int D, bool FAST>
+constexpr bool rel_kv_planes3() {
+  return sizeof(T) == 4 && !FAST && D == 32;
+}
+
+template <typename T, int D, int QW, int BN, int VBUFS, bool KV_DIRECT = false, bool PLANES3 = false>
 struct RelLayout {
   static constexpr int BM = kWaves * QW;                // query rows per workgroup
   static constexpr int NCC = (QW + BN - 1 + 15) / 16;   // c2p window chunks per wavefront
@@ -357,10 +365,13 @@ struct RelLayout {
   static constexpr int CW_LD = NCC == 5 ? 88 : 16 * NCC + 4;  // Cw[wave][QW][CW_LD]
   static constexpr int PW_LD = 16 * NPC + 20;                 // Pw[BN][PW_LD]
 
-  static constexpr int VT_SIZE = BN * VS_LD;            // elements of one V tile buffer
+  // Elements of T in one K tile and in one V tile buffer (three bf16 planes
+  // take 1.5 times the fp32 tile).
+  static constexpr int KS_SIZE = PLANES3 ? BN * KS_LD * 3 / 2 : BN * KS_LD;
+  static constexpr int VT_SIZE = PLANES3 ? BN * VS_LD * 3 / 2 : BN * VS_LD;
 
   static constexpr size_t ks_off = 0;
-  static constexpr size_t vt_off = ks_off + size_t(BN) * KS_LD * sizeof(T);
+  static constexpr size_t vt_off = ks_off + size_t(KS_SIZE) * sizeof(T);
   static constexpr size_t pw_off = vt_off + VBUFS * size_t(VT_SIZE) * sizeof(T);
   static constexpr size_t cw_off = pw_off + size_t(BN) * PW_LD * sizeof(T);
   static constexpr size_t bytes = cw_off + size_t(kWaves) * QW * CW_LD * sizeof(T);
@@ -394,7 +405,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
   constexpr bool kDirect = rel_kv_direct<T, D, VBUFS, TABLE, P2C>();
-  using LY = RelLayout<T, D, QW, BN, VBUFS, kDirect>;
+  // Strict fp32 at d = 32: K and V staged as three bf16 planes (split once per
+  // workgroup instead of once per reading wavefront).
+  constexpr bool PL3 = rel_kv_planes3<T, D, FAST>();
+  static_assert(!PL3 || EXACT, "three planes feed the bf16x6 products");
+  // K and V staged split (FAST: hi, lo; PL3: hi, mid, lo planes).
+  constexpr bool kPlanes = FAST || PL3;
+  using LY = RelLayout<T, D, QW, BN, VBUFS, kDirect, PL3>;
   constexpr int BM = LY::BM;
   constexpr int kQB = QW / 16;          // 16-query MFMA blocks per wavefront
   constexpr int KB = BN / 16;           // 16-key blocks per tile
@@ -774,6 +791,22 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     hi = __builtin_bit_cast(u32x2_t, h);
     lo = __builtin_bit_cast(u32x2_t, l);
   };
+  // Strict fp32 at d = 32: the three planes of RelMmaExact (hi, mid, lo), each
+  // BN rows of the tile's pitch, one after the other.
+  auto split_chunk3 = [](const u32x4_t& raw, u32x2_t& hi, u32x2_t& mid, u32x2_t& lo) {
+    const f32x4_t x = __builtin_bit_cast(f32x4_t, raw);
+    bf16x4_t h, m, l;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = static_cast<__bf16>(x[e]);
+      const float r = x[e] - static_cast<float>(h[e]);
+      m[e] = static_cast<__bf16>(r);
+      l[e] = static_cast<__bf16>(r - static_cast<float>(m[e]));
+    }
+    hi = __builtin_bit_cast(u32x2_t, h);
+    mid = __builtin_bit_cast(u32x2_t, m);
+    lo = __builtin_bit_cast(u32x2_t, l);
+  };
   auto stage_k = [&]() {
 #pragma unroll
     for (int n = 0; n < NCH; ++n)
@@ -784,6 +817,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           split_chunk(pk[n], hi, lo);
           *reinterpret_cast<u32x2_t*>(kh + kls[n]) = hi;
           *reinterpret_cast<u32x2_t*>(kh + BN * LY::KS_LD + kls[n]) = lo;
+        } else if constexpr (PL3) {
+          __bf16* kh = reinterpret_cast<__bf16*>(Ks);
+          u32x2_t hi, mid, lo;
+          split_chunk3(pk[n], hi, mid, lo);
+          *reinterpret_cast<u32x2_t*>(kh + kls[n]) = hi;
+          *reinterpret_cast<u32x2_t*>(kh + BN * LY::KS_LD + kls[n]) = mid;
+          *reinterpret_cast<u32x2_t*>(kh + 2 * BN * LY::KS_LD + kls[n]) = lo;
         } else {
           *reinterpret_cast<u32x4_t*>(Ks + kls[n]) = pk[n];
         }
@@ -806,6 +846,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       const __bf16* kh = reinterpret_cast<const __bf16*>(Ks);
       return QF{*reinterpret_cast<const bf16x8_t*>(kh + off),
                 *reinterpret_cast<const bf16x8_t*>(kh + BN * LY::KS_LD + off)};
+    } else if constexpr (PL3) {
+      const int off = row * LY::KS_LD + 32 * kd + 8 * g;
+      const __bf16* kh = reinterpret_cast<const __bf16*>(Ks);
+      return QF{*reinterpret_cast<const bf16x8_t*>(kh + off),
+                *reinterpret_cast<const bf16x8_t*>(kh + BN * LY::KS_LD + off),
+                *reinterpret_cast<const bf16x8_t*>(kh + 2 * BN * LY::KS_LD + off)};
     } else {
       return QF{};  // not used by the other instances
     }
@@ -822,6 +868,13 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
           split_chunk(pv[n], hi, lo);
           *reinterpret_cast<u32x2_t*>(vh + vls[n]) = hi;
           *reinterpret_cast<u32x2_t*>(vh + BN * LY::VS_LD + vls[n]) = lo;
+        } else if constexpr (PL3) {
+          __bf16* vh = reinterpret_cast<__bf16*>(vs);
+          u32x2_t hi, mid, lo;
+          split_chunk3(pv[n], hi, mid, lo);
+          *reinterpret_cast<u32x2_t*>(vh + vls[n]) = hi;
+          *reinterpret_cast<u32x2_t*>(vh + BN * LY::VS_LD + vls[n]) = mid;
+          *reinterpret_cast<u32x2_t*>(vh + 2 * BN * LY::VS_LD + vls[n]) = lo;
         } else {
           *reinterpret_cast<u32x2_t*>(vs + vls[n]) = u32x2_t{pv[n][0], pv[n][1]};
           *reinterpret_cast<u32x2_t*>(vs + vls[n] + E16 / 2) = u32x2_t{pv[n][2], pv[n][3]};
@@ -1163,7 +1216,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
       QF kfa[2][KD];
 #pragma unroll
       for (int kd = 0; kd < KD; ++kd) {
-        if constexpr (FAST) {
+        if constexpr (kPlanes) {
           kfa[0][kd] = k_read(key_of(c), kd);
         } else {
           kfa[0][kd] = to_q(*reinterpret_cast<const F*>(Ks + k_elem(key_of(c), kd)));
@@ -1177,7 +1230,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         if (kb + 1 < KB) {
 #pragma unroll
           for (int kd = 0; kd < KD; ++kd) {
-            if constexpr (FAST) {
+            if constexpr (kPlanes) {
               kfa[(kb + 1) & 1][kd] = k_read(16 * (kb + 1) + key_of(c), kd);
             } else {
               kfa[(kb + 1) & 1][kd] = to_q(*reinterpret_cast<const F*>(Ks + k_elem(16 * (kb + 1) + key_of(c), kd)));
@@ -1225,7 +1278,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         QF kf[KD];
 #pragma unroll
         for (int kd = 0; kd < KD; ++kd) {
-          if constexpr (FAST) {
+          if constexpr (kPlanes) {
             kf[kd] = k_read(16 * kb + key_of(c), kd);
           } else {
             kf[kd] = to_q(*reinterpret_cast<const F*>(Ks + k_elem(16 * kb + key_of(c), kd)));
@@ -1393,6 +1446,11 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         const __bf16* vh = reinterpret_cast<const __bf16*>(vt_cur);
         return QF{__builtin_bit_cast(bf16x8_t, vt_tr16(vh, ks, db)),
                   __builtin_bit_cast(bf16x8_t, vt_tr16(vh + BN * LY::VS_LD, ks, db))};
+      } else if constexpr (PL3) {
+        const __bf16* vh = reinterpret_cast<const __bf16*>(vt_cur);
+        return QF{__builtin_bit_cast(bf16x8_t, vt_tr16(vh, ks, db)),
+                  __builtin_bit_cast(bf16x8_t, vt_tr16(vh + BN * LY::VS_LD, ks, db)),
+                  __builtin_bit_cast(bf16x8_t, vt_tr16(vh + 2 * BN * LY::VS_LD, ks, db))};
       } else if constexpr (sizeof(T) == 4) {
         // fp32: element e holds V[key][16db + c] for the keys of the P^T
         // operand, 32ks + g + 4e (e < 4) and 32ks + 16 + g + 4(e - 4).
@@ -1726,7 +1784,8 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
   constexpr int VB = rel_v_buffers<T, D, QW>();
   constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
-  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE, P2C>()>;
+  using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE, P2C>(),
+                       rel_kv_planes3<T, D, FAST>()>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
