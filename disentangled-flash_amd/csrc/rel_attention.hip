@@ -338,12 +338,13 @@ __device__ constexpr int kv_swizzle(int row) {
   return D == 64 ? ((b0 ^ b1) | (a << 1)) : (b0 | (a << 1) | (b0 << 3));
 }
 
-// Strict fp32 at d = 32 stages K and V already split into three bf16 planes
-// (hi, mid, lo: 6 bytes per element, 1.5 times the fp32 tile), which fits the
-// LDS at this head size only (d = 64 fills it with the fp32 tiles).
+// Strict fp32 at d <= 64 stages K and V already split into three bf16 planes
+// (hi, mid, lo: 6 bytes per element, 1.5 times the fp32 tile).  At d = 64 this
+// fits the LDS with one V buffer (159 KB per workgroup; two fp32 V buffers
+// without planes measured the same as one).
 template <typename T, int D, bool FAST>
 constexpr bool rel_kv_planes3() {
-  return sizeof(T) == 4 && !FAST && D == 32;
+  return sizeof(T) == 4 && !FAST && D <= 64;
 }
 
 template <typename T, int D, int QW, int BN, int VBUFS, bool KV_DIRECT = false, bool PLANES3 = false>
@@ -405,7 +406,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
   constexpr bool kDirect = rel_kv_direct<T, D, VBUFS, TABLE, P2C>();
-  // Strict fp32 at d = 32: K and V staged as three bf16 planes (split once per
+  // Strict fp32 at d <= 64: K and V staged as three bf16 planes (split once per
   // workgroup instead of once per reading wavefront).
   constexpr bool PL3 = rel_kv_planes3<T, D, FAST>();
   static_assert(!PL3 || EXACT, "three planes feed the bf16x6 products");
@@ -426,6 +427,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   constexpr int NPC = LY::NPC;
   constexpr uint32_t ES = sizeof(T);
   static_assert(BN % 32 == 0 && BN <= 64, "key tile must be 32 or 64 keys");
+  static_assert(LY::bytes * WGS <= 160 * 1024, "workgroups per CU fit the 160 KB of LDS");
   static_assert(QW % 16 == 0, "query rows per wavefront must be a multiple of 16");
   static_assert(NKC % kThreads == 0 || NKC < kThreads, "K tile must split evenly over the workgroup");
   static_assert(!kDirect || NKC % kThreads == 0, "direct copies: whole rounds of 64 chunks per wavefront");
@@ -791,7 +793,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     hi = __builtin_bit_cast(u32x2_t, h);
     lo = __builtin_bit_cast(u32x2_t, l);
   };
-  // Strict fp32 at d = 32: the three planes of RelMmaExact (hi, mid, lo), each
+  // Strict fp32 at d <= 64: the three planes of RelMmaExact (hi, mid, lo), each
   // BN rows of the tile's pitch, one after the other.
   auto split_chunk3 = [](const u32x4_t& raw, u32x2_t& hi, u32x2_t& mid, u32x2_t& lo) {
     const f32x4_t x = __builtin_bit_cast(f32x4_t, raw);
@@ -1721,8 +1723,9 @@ constexpr int rel_block_n() {
 // same; at QW = 16 one buffer lets three workgroups share a CU (48 KB each).
 // fp32 (twice the LDS per element, eight MFMAs per k-step) runs one workgroup
 // per CU with up to 512 registers per lane: two V buffers except at d = 128.
-template <typename T, int D, int QW>
+template <typename T, int D, int QW, bool FAST = false>
 constexpr int rel_v_buffers() {
+  if constexpr (rel_kv_planes3<T, D, FAST>() && D == 64) return 1;
   return (D >= 128 || (QW == 16 && sizeof(T) == 2)) ? 1 : 2;
 }
 template <typename T, int D, int QW>
@@ -1782,7 +1785,7 @@ __global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __res
 template <typename T, int D, int QW, bool C2P, bool P2C, bool FAST = false, bool TABLE = false>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
-  constexpr int VB = rel_v_buffers<T, D, QW>();
+  constexpr int VB = rel_v_buffers<T, D, QW, FAST>();
   constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
   using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE, P2C>(),
                        rel_kv_planes3<T, D, FAST>()>;
