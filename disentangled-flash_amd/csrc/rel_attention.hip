@@ -338,13 +338,22 @@ __device__ constexpr int kv_swizzle(int row) {
   return D == 64 ? ((b0 ^ b1) | (a << 1)) : (b0 | (a << 1) | (b0 << 3));
 }
 
-// Strict fp32 at d <= 64 stages K and V already split into three bf16 planes
-// (hi, mid, lo: 6 bytes per element, 1.5 times the fp32 tile).  At d = 64 this
-// fits the LDS with one V buffer (159 KB per workgroup; two fp32 V buffers
-// without planes measured the same as one).
-template <typename T, int D, bool FAST>
+// Strict fp32 on the bf16 matrix unit (bf16x6 products, RelMmaExact): at
+// d <= 64, and at d = 128 without the c2p term (with it, the split fragments
+// spill; measured there, C5 c2p alone ran 345 against 327 us on the fp32 MFMA,
+// p2c alone 232 against 275, neither term 172 against 189).
+template <typename T, int D, bool FAST, bool C2P>
+constexpr bool rel_exact_fp32() {
+  return sizeof(T) == 4 && !FAST && (D <= 64 || !C2P);
+}
+// Strict fp32 on the bf16 unit stages K and V already split into three bf16
+// planes (hi, mid, lo: 6 bytes per element, 1.5 times the fp32 tile).  At
+// d = 64 this fits the LDS with one V buffer (159 KB per workgroup; two fp32 V
+// buffers without planes measured the same as one), at d = 128 with 512 bytes
+// to spare.
+template <typename T, int D, bool FAST, bool C2P>
 constexpr bool rel_kv_planes3() {
-  return sizeof(T) == 4 && !FAST && D <= 64;
+  return rel_exact_fp32<T, D, FAST, C2P>();
 }
 
 template <typename T, int D, int QW, int BN, int VBUFS, bool KV_DIRECT = false, bool PLANES3 = false>
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   constexpr bool MC = C2P && !TABLE;
   constexpr bool MP = P2C && !TABLE;
   // fp32 on the bf16 matrix unit: bf16x3 (FAST) or bf16x6 (strict, EXACT).
-  constexpr bool EXACT = sizeof(T) == 4 && !FAST && D <= 64;
+  constexpr bool EXACT = rel_exact_fp32<T, D, FAST, C2P>();
   constexpr bool SPLITQ = FAST || EXACT;
   using M = std::conditional_t<FAST, RelMmaFast, std::conditional_t<EXACT, RelMmaExact, RelMma<T>>>;
   using F = typename M::frag;
@@ -406,9 +415,9 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   };
   constexpr int E16 = kChunkElems<T>;   // elements per 16-byte chunk
   constexpr bool kDirect = rel_kv_direct<T, D, VBUFS, TABLE, P2C>();
-  // Strict fp32 at d <= 64: K and V staged as three bf16 planes (split once per
-  // workgroup instead of once per reading wavefront).
-  constexpr bool PL3 = rel_kv_planes3<T, D, FAST>();
+  // Strict fp32 on the bf16 unit: K and V staged as three bf16 planes (split
+  // once per workgroup instead of once per reading wavefront).
+  constexpr bool PL3 = rel_kv_planes3<T, D, FAST, C2P>();
   static_assert(!PL3 || EXACT, "three planes feed the bf16x6 products");
   // K and V staged split (FAST: hi, lo; PL3: hi, mid, lo planes).
   constexpr bool kPlanes = FAST || PL3;
@@ -793,7 +802,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
     hi = __builtin_bit_cast(u32x2_t, h);
     lo = __builtin_bit_cast(u32x2_t, l);
   };
-  // Strict fp32 at d <= 64: the three planes of RelMmaExact (hi, mid, lo), each
+  // Strict fp32 on the bf16 unit: the three planes of RelMmaExact (hi, mid, lo), each
   // BN rows of the tile's pitch, one after the other.
   auto split_chunk3 = [](const u32x4_t& raw, u32x2_t& hi, u32x2_t& mid, u32x2_t& lo) {
     const f32x4_t x = __builtin_bit_cast(f32x4_t, raw);
@@ -1723,9 +1732,9 @@ constexpr int rel_block_n() {
 // same; at QW = 16 one buffer lets three workgroups share a CU (48 KB each).
 // fp32 (twice the LDS per element, eight MFMAs per k-step) runs one workgroup
 // per CU with up to 512 registers per lane: two V buffers except at d = 128.
-template <typename T, int D, int QW, bool FAST = false>
+template <typename T, int D, int QW, bool FAST, bool C2P>
 constexpr int rel_v_buffers() {
-  if constexpr (rel_kv_planes3<T, D, FAST>() && D == 64) return 1;
+  if constexpr (rel_kv_planes3<T, D, FAST, C2P>() && D == 64) return 1;
   return (D >= 128 || (QW == 16 && sizeof(T) == 2)) ? 1 : 2;
 }
 template <typename T, int D, int QW>
@@ -1785,10 +1794,10 @@ __global__ __launch_bounds__(256) void rel_split_merge_kernel(const float* __res
 template <typename T, int D, int QW, bool C2P, bool P2C, bool FAST = false, bool TABLE = false>
 int launch_rel(const RelParams& base, hipStream_t stream) {
   constexpr int BN = rel_block_n<D>();
-  constexpr int VB = rel_v_buffers<T, D, QW, FAST>();
+  constexpr int VB = rel_v_buffers<T, D, QW, FAST, C2P>();
   constexpr int WGS = rel_workgroups_per_cu<T, D, QW>();
   using LY = RelLayout<T, D, QW, BN, VB, rel_kv_direct<T, D, VB, TABLE, P2C>(),
-                       rel_kv_planes3<T, D, FAST>()>;
+                       rel_kv_planes3<T, D, FAST, C2P>()>;
   RelParams prm = base;
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,

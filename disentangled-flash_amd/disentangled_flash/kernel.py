@@ -343,8 +343,9 @@ class HipInferenceDisentangledSelfAttention(TorchInferenceDisentangledSelfAttent
 
     Head dimensions 32, 64 and 128; fp16, bf16 and fp32.  ``fp32_precision``
     follows the reference (``kernel.py:485-493``): ``"strict"`` gives fp32-accurate
-    products (IEEE fp32 MFMA at d = 128; at d <= 64 six bf16 MFMAs over a
-    three-way bf16 split of each operand, which keeps all 24 significand bits);
+    products (IEEE fp32 MFMA at d = 128 with the c2p term; otherwise six bf16
+    MFMAs over a three-way bf16 split of each operand, which keeps all 24
+    significand bits);
     ``"fast"`` is TF32 there, and gfx950 has no TF32 matrix path, so the fused
     kernel splits each fp32 operand into bf16 hi + lo and runs every product as
     three bf16 MFMAs (relative error about 2^-16 per product, below TF32's

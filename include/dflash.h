@@ -98,7 +98,8 @@ DFLASH_API int dflash_attention_fwd(const void* query, const void* key, const vo
  *   strict_fp32       : fp32 only.  1 = the reference's strict mode
  *                       (input_precision="ieee", kernel.py:216): fp32-accurate
  *                       products, IEEE fp32 MFMA (v_mfma_f32_16x16x4_f32) at
- *                       D = 128 and, at D <= 64, six bf16 MFMAs over a
+ *                       D = 128 with the c2p term and, otherwise, six bf16
+ *                       MFMAs over a
  *                       three-way bf16 split of each operand (all 24 significand
  *                       bits; the dropped part products are below 2^-24 of the
  *                       leading one).  0 = the reference's fast mode, which is
