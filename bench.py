@@ -489,7 +489,7 @@ def kernel_inputs(shape: str, dtype):
 def bench_tile_sweep(steps: int, warmup: int):
     """Per-shape tile evidence: the fused fp16 op (c2p|p2c, no split) over batch sizes for
     d=64 (H=12, L=512), d=32 (H=16, L=384) and d=128 (H=8, L=512).  The tile the library
-    picks can be forced per process with DFLASH_REL_QW=16 or 32 (d=32 only has both)."""
+    picks can be forced per process with DFLASH_REL_QW=16 or 32 (d=32 and 16-bit d=128 have both)."""
 
     import os
 

@@ -99,7 +99,8 @@ int dflash_attention_fwd(const void* query, const void* key, const void* value, 
   rp.has_c2p = has_c2p;
   rp.has_p2c = has_p2c;
   rp.splits = 1;
-  rp.qw = 32;
+  // The table form keeps the 16-row tile at d = 128 (two workgroups per CU).
+  rp.qw = D >= 128 ? 16 : 32;
   // fp32 with strict_fp32 = 0: QK and PV on the bf16x3 products (the
   // reference's TF32 mode, kernel.py:222); the windows are read, not multiplied.
   rp.fast = (dtype == DFLASH_DTYPE_FP32 && !strict_fp32) ? 1 : 0;
@@ -187,7 +188,7 @@ int rel_forward(const void* query, const void* key, const void* value, int64_t s
   rp.has_c2p = has_c2p;
   rp.has_p2c = has_p2c;
   rp.splits = 1;
-  rp.qw = rel_attention_qw(B, H, L, D, current_device_cus());
+  rp.qw = rel_attention_qw(B, H, L, D, current_device_cus(), has_c2p != 0);
   rp.fast = dtype == DFLASH_DTYPE_FP32 && !strict_fp32;
   if (splits > 1 && dtype != DFLASH_DTYPE_FP32) {  // fp32 runs unsplit
     if (splits > 8) return DFLASH_ERR_SHAPE;

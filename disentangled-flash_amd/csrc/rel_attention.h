@@ -27,8 +27,8 @@ struct RelParams {
   int splits;
   int split_tiles;
   float* part;
-  // Query rows per wavefront of the unsplit form at d <= 64: 32 (default) or
-  // 16 (rel_attention_qw); d = 128 always runs 16.
+  // Query rows per wavefront of the unsplit form: 32 (default) or 16
+  // (rel_attention_qw); fp32 at d = 128 always runs 16.
   int qw;
   // fp32 only: 1 = products on the bf16 matrix unit in three parts
   // (fp32_precision="fast"), 0 = IEEE fp32 MFMA.
@@ -55,6 +55,7 @@ size_t rel_attention_workspace_bytes(int splits, int B, int H, int L, int D);
 
 // Query rows per wavefront for an unsplit launch (32 or 16) on a device with
 // `cus` CUs, from the measured per-shape table in rel_attention.hip.
-int rel_attention_qw(int B, int H, int L, int D, int cus);
+// `has_c2p`: the c2p term is computed (the 32-row d = 128 tile pays only then).
+int rel_attention_qw(int B, int H, int L, int D, int cus, bool has_c2p);
 
 }  // namespace dflash

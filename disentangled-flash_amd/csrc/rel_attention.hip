@@ -1735,11 +1735,11 @@ constexpr int rel_block_n() {
 template <typename T, int D, int QW, bool FAST, bool C2P>
 constexpr int rel_v_buffers() {
   if constexpr (rel_kv_planes3<T, D, FAST, C2P>() && D == 64) return 1;
-  return (D >= 128 || (QW == 16 && sizeof(T) == 2)) ? 1 : 2;
+  return ((D >= 128 && QW == 16) || (QW == 16 && sizeof(T) == 2)) ? 1 : 2;
 }
 template <typename T, int D, int QW>
 constexpr int rel_workgroups_per_cu() {
-  if constexpr (sizeof(T) == 4) return 1;
+  if constexpr (sizeof(T) == 4 || (D >= 128 && QW == 32)) return 1;
   return (D <= 64 && QW == 16) ? 3 : 2;
 }
 
@@ -1802,7 +1802,7 @@ int launch_rel(const RelParams& base, hipStream_t stream) {
   prm.nqb = (prm.L + LY::BM - 1) / LY::BM;
   // The split-key form exists for the default 16-bit tile (QW = 32 at d <= 64,
   // 16 at d = 128); fp32 never splits.
-  constexpr bool kSplitBuilt = sizeof(T) == 2 && ((D >= 128) || QW == 32) && !TABLE;
+  constexpr bool kSplitBuilt = sizeof(T) == 2 && (D >= 128 ? QW == 16 : QW == 32) && !TABLE;
   constexpr auto kernel = rel_attention_kernel<T, D, QW, BN, VB, WGS, C2P, P2C, false, FAST, TABLE>;
   if (prm.splits < 1) prm.splits = 1;
   if (!kSplitBuilt && prm.splits > 1) return DFLASH_ERR_SHAPE;
@@ -1874,13 +1874,18 @@ int rel_modes_qw(const RelParams& prm, hipStream_t stream) {
   return launch_rel<T, D, QW, false, false, FAST>(prm, stream);
 }
 
-// d = 128 has only QW = 16; d = 32 runs QW = 16 when prm.qw asks for it (only
+// 16-bit d = 128 runs QW = 32 (one workgroup per CU, 512 registers per lane)
+// when prm.qw asks for it, unsplit; the split instance and fp32 keep QW = 16.
+// d = 32 runs QW = 16 when prm.qw asks for it (only
 // for the unsplit form: the split instances are built for QW = 32); d = 64 has
 // only QW = 32 (QW = 16 measured 1.2-2.5x slower at every batch, see
 // rel_attention_qw).
 template <typename T, int D>
 int rel_modes(const RelParams& prm, hipStream_t stream) {
-  if constexpr (D >= 128) {
+  if constexpr (D >= 128 && sizeof(T) == 2) {
+    if (prm.qw == 32 && prm.splits <= 1) return rel_modes_qw<T, D, 32>(prm, stream);
+    return rel_modes_qw<T, D, 16>(prm, stream);
+  } else if constexpr (D >= 128) {
     return rel_modes_qw<T, D, 16>(prm, stream);
   } else if constexpr (D == 32 && sizeof(T) == 2) {
     if (prm.qw == 16 && prm.splits <= 1) return rel_modes_qw<T, D, 16>(prm, stream);
@@ -1916,14 +1921,23 @@ int rel_attention_splits(int B, int H, int L, int D, int cus, int* split_tiles) 
   return (tiles + st - 1) / st;
 }
 
-int rel_attention_qw(int B, int H, int L, int D, int cus) {
-  if (D >= 128) return 16;
+int rel_attention_qw(int B, int H, int L, int D, int cus, bool has_c2p) {
   // DFLASH_REL_QW=16 or 32 forces the tile (measurement runs only).
   static const int forced = [] {
     const char* env = std::getenv("DFLASH_REL_QW");
     return env ? std::atoi(env) : 0;
   }();
   if (forced == 16 || forced == 32) return forced;
+  // d = 128 (16-bit): QW = 32 at one workgroup per CU (512 registers per lane)
+  // against QW = 16 at two.  Each wavefront loads the relative rows of its own
+  // c2p window, so 32 rows per wavefront halve those loads per query; the tile
+  // pays with the c2p term and a grid that fills the CUs (C5, H = 8, L = 512,
+  // c2p|p2c: B = 8 39.5 against 46.8 us, B = 16 76.0 against 86.9, B = 32
+  // 148.8 against 166.9; B = 4 38.8 against 26.4; p2c alone 54.1 against 48.1).
+  if (D >= 128) {
+    const int64_t wg32 = static_cast<int64_t>((L + 127) / 128) * B * H;
+    return (has_c2p && cus > 0 && wg32 >= cus) ? 32 : 16;
+  }
   // Measured table (MI355X, 256 CUs, fp16, c2p|p2c; kernel time of back-to-back
   // launches, QW = 32 against QW = 16):
   //   d = 64, H = 12, L = 512, B = 1..48: QW = 32 wins everywhere (QW = 16 at

@@ -557,3 +557,50 @@ def test_qw16_tile_forced_parity_subprocess():
                             text=True, timeout=240)
     assert result.returncode == 0, result.stdout[-2000:] + result.stderr[-4000:]
     assert "qw16 ok" in result.stdout
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("mode", ["both", "c2p"])
+def test_d128_tile_table_selects_qw32(dtype, mode):
+    """C5 d=128 (H=8, L=512) at B=8 with the c2p term: the per-shape table picks
+    the 32-row tile at one workgroup per CU (256 workgroups fill the CUs)."""
+
+    has_c2p, has_p2c = MODES[mode]
+    args = _inputs(8, 8, 512, 128, DTYPES[dtype], "boundary", seed=128)
+    out = _run_rel(*args, has_c2p, has_p2c)
+    _check(out, *args, has_c2p, has_p2c, f"d128 B=8 qw32 {dtype} {mode}")
+
+
+QW32_D128_SCRIPT = r"""
+import math, sys, torch
+sys.path[:0] = [{repo!r}, {pkg!r}, {tests!r}]
+import test_gpu_attention as t
+for dtype in (torch.float16, torch.bfloat16):
+    for pattern in ("right", "left", "holes", "middle", "all", "boundary"):
+        for mode, (c2p, p2c) in t.MODES.items():
+            for batch, length in ((2, 200), (3, 1), (2, 65), (1, 700)):
+                args = t._inputs(batch, 2, length, 128, dtype, pattern, seed=length + batch)
+                out = t._run_rel(*args, c2p, p2c, 1)
+                t._check(out, *args, c2p, p2c, f"qw32 d128 {{dtype}} {{pattern}} {{mode}} B={{batch}} L={{length}}")
+print("qw32 d128 ok", flush=True)
+"""
+
+
+def test_qw32_d128_tile_forced_parity_subprocess():
+    """Every mode, mask pattern and length on the 32-row d=128 tile, forced by
+    DFLASH_REL_QW=32 in a child process (the tile is chosen once per process)."""
+
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    tests = Path(__file__).resolve().parent
+    repo = tests.parent
+    script = QW32_D128_SCRIPT.format(repo=str(repo), pkg=str(repo / "disentangled-flash_amd"),
+                                     tests=str(tests))
+    env = dict(os.environ, DFLASH_REL_QW="32")
+    result = subprocess.run([sys.executable, "-c", script], env=env, capture_output=True,
+                            text=True, timeout=240)
+    assert result.returncode == 0, result.stdout[-2000:] + result.stderr[-4000:]
+    assert "qw32 d128 ok" in result.stdout
