@@ -1216,10 +1216,12 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
 
     // ---- S^T = K . Q^T and the p2c window Pw[jr][t] = Qr[slot(dlo + t)] . K_jr ----
     f32x4_t sc[KB][kQB];
-    // For d <= 64 one straight-line copy per wavefront index, so that the
-    // chunks a wavefront skips are known at compile time and the MFMAs of the
-    // whole phase form one scheduling region.  d = 128 keeps one copy with
-    // runtime skips (below): with four copies it runs out of registers.
+    // For d <= 64, and d = 128 on the 32-row tile (512 registers per lane), one
+    // straight-line copy per wavefront index, so that the chunks a wavefront
+    // skips are known at compile time and the MFMAs of the whole phase form one
+    // scheduling region (d = 128, C5: 75.8 -> 72.1 us).  The 16-row d = 128
+    // tile keeps one copy with runtime skips (below): with four copies it runs
+    // out of its 256 registers.
     auto qk_p2c = [&](auto wave_c) {
       constexpr int W = decltype(wave_c)::value;
       // K fragments one key block ahead (two register sets), so that the
@@ -1276,7 +1278,7 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
         for (int kd = 0; kd < KD; ++kd) prow[0][kd] = to_q(prow_in[kd]);
       }
     }
-    if constexpr (D <= 64) {
+    if constexpr (D <= 64 || QW == 32) {
       switch (wave) {
         case 0: qk_p2c(IntC<0>{}); break;
         case 1: qk_p2c(IntC<1>{}); break;
