@@ -37,8 +37,9 @@ struct RelParams {
   // (the reference op's contract) instead of the relative rows [H, S, D].
   // Unsplit, QW = 32 (d <= 64) or 16 (d = 128), IEEE fp32.
   int table;
-  // First (b, h) group of the launch (the table form's last slice may run as
-  // a launch of its own); 0 otherwise.
+  // First group of the launch, groups numbered h * B + b (the table form's
+  // last slice, b = B - 1 and h = H - 1, may run as a launch of its own); 0
+  // otherwise.
   int bh0;
 };
 

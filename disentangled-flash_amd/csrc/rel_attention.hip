@@ -459,9 +459,15 @@ __global__ __launch_bounds__(kThreads, WGS) void rel_attention_kernel(RelParams 
   const int split = SPLIT ? mk % p.splits : 0;
   const int m = SPLIT ? mk / p.splits : mk;
   const int qblk = m % p.nqb;
+  // Groups of query blocks in head-major order (the batch index fastest):
+  // each XCD's contiguous range of groups then holds sequences of every
+  // length of the batch, not a few neighbouring ones, so the XCDs finish
+  // together on ragged batches (C5 valid-length cycle: d = 128 71.8 -> 53.1
+  // us, d = 32 28.3 -> 21.5 us; unpadded unchanged).  A group's query blocks
+  // stay on one XCD.  The last group is the last (b, h) slice either way.
   const int bh = p.bh0 + m / p.nqb;
-  const int b = bh / p.H;
-  const int h = bh - b * p.H;
+  const int h = bh / p.B;
+  const int b = bh - h * p.B;
   const int i0 = qblk * BM;
   const int i0w = i0 + wave * QW;
   const uint32_t sl_bytes = static_cast<uint32_t>(p.sl) * ES;
