@@ -1734,12 +1734,14 @@ template <int D>
 constexpr int rel_block_n() {
   return 64;
 }
-// d = 128 keeps one V buffer so that two workgroups fit in the LDS of a CU
-// (65 KB each instead of 82 KB): 153 -> 117 us at B=16, L=512, H=8, fp16.
-// For d <= 64 at QW = 32 (two workgroups either way) both placements time the
-// same; at QW = 16 one buffer lets three workgroups share a CU (48 KB each).
-// fp32 (twice the LDS per element, eight MFMAs per k-step) runs one workgroup
-// per CU with up to 512 registers per lane: two V buffers except at d = 128.
+// d = 128 on the 16-row tile keeps one V buffer so that two workgroups fit in
+// the LDS of a CU (65 KB each instead of 82 KB): 153 -> 117 us at B=16, L=512,
+// H=8, fp16; the 32-row tile (one workgroup per CU) takes two.  For d <= 64 at
+// QW = 32 (two workgroups either way) both placements time the same; at
+// QW = 16 one buffer lets three workgroups share a CU (48 KB each).  fp32
+// (twice the LDS per element) runs one workgroup per CU with up to 512
+// registers per lane: two V buffers except at d = 128 and where the three bf16
+// planes of K and V need the room (strict, d = 64).
 template <typename T, int D, int QW, bool FAST, bool C2P>
 constexpr int rel_v_buffers() {
   if constexpr (rel_kv_planes3<T, D, FAST, C2P>() && D == 64) return 1;
